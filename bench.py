@@ -1,0 +1,229 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+One step = one Qwen3-8B-shape causal GQA prefill (S 4096, 32 q / 8 kv
+heads, d 128, fp16, Q/K after per-head RMSNorm + RoPE) followed by one batch-32 paged
+decode (config 4: 32 q / 8 kv heads, d 128, KV lengths U[512, 4096], block 16, fp16).
+
+`value` is the prefill throughput in TFLOP/s (algorithmic FLOPs 4*d*Hq*S(S+1)/2 per
+call); the decode KV-read bandwidth (4096 * sum(L) bytes per call) is reported under
+`decode`.  Inputs are synthetic and resident in HBM before timing starts.  The decode
+reads one of several KV pools in rotation so that the 256 MB last-level cache does not
+serve it.  Each kernel's mean launch time is measured with HIP events on the stream the
+kernels run on; `ms_per_step` is the wall time of the K timed steps.
+
+The CPU baseline runs the oracle (oracle/oracle.c, a restatement of the reference's CPU
+MHA) on a bounded sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, TFLOP/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
+    return ap.parse_args()
+
+
+def rmsnorm_rope(x, H, d, theta=1e6):
+    """Per-head RMSNorm (unit weight, eps 1e-6) then rotate-half RoPE, on the GPU (input
+    synthesis only)."""
+    import torch
+    S = x.shape[0]
+    x = x.view(S, H, d).float()
+    x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+    half = d // 2
+    freq = 1.0 / theta ** (torch.arange(0, half, device=x.device, dtype=torch.float32) * 2 / d)
+    ang = torch.arange(S, device=x.device, dtype=torch.float32)[:, None] * freq[None]
+    c, s = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+    x0, x1 = x[..., :half], x[..., half:]
+    return torch.cat([c * x0 - s * x1, c * x1 + s * x0], -1).reshape(S, H * d)
+
+
+def make_prefill(dtype, gen):
+    import torch
+    S, Hq, Hkv, d = 4096, 32, 8, 128
+    dev = "cuda"
+    q = rmsnorm_rope(torch.randn(S, Hq * d, device=dev, generator=gen), Hq, d).to(dtype)
+    k = rmsnorm_rope(torch.randn(S, Hkv * d, device=dev, generator=gen), Hkv, d).to(dtype)
+    v = torch.randn(S, Hkv * d, device=dev, generator=gen).to(dtype)
+    o = torch.empty_like(q)
+    flops = 4.0 * d * Hq * S * (S + 1) / 2
+    return dict(S=S, Hq=Hq, Hkv=Hkv, d=d, q=q, k=k, v=v, o=o, flops=flops)
+
+
+def make_decode(dtype, gen, pools):
+    import numpy as np
+    import torch
+    B, Hq, Hkv, d, bs = 32, 32, 8, 128, 16
+    rng = np.random.default_rng(0xC4)
+    lens = rng.integers(512, 4097, B).astype(np.int32)
+    nblk = (lens + bs - 1) // bs
+    total = int(nblk.sum())
+    maxb = int(nblk.max())
+    bt = np.zeros((B, maxb), np.int32)
+    perm = rng.permutation(total).astype(np.int32)
+    off = 0
+    for b in range(B):
+        bt[b, : nblk[b]] = perm[off: off + nblk[b]]
+        off += nblk[b]
+    kp = [torch.randn(total, bs, Hkv, d, device="cuda", generator=gen).to(dtype)
+          for _ in range(pools)]
+    vp = [torch.randn(total, bs, Hkv, d, device="cuda", generator=gen).to(dtype)
+          for _ in range(pools)]
+    q = torch.randn(B, Hq, d, device="cuda", generator=gen).to(dtype)
+    o = torch.empty_like(q)
+    kv_bytes = 2 * int(lens.sum()) * Hkv * d * 2  # K and V, read once per kv head
+    return dict(B=B, Hq=Hq, Hkv=Hkv, d=d, bs=bs, lens=lens, lens_d=torch.from_numpy(lens).cuda(),
+                bt=torch.from_numpy(bt).cuda(), kp=kp, vp=vp, q=q, o=o, kv_bytes=kv_bytes,
+                maxlen=int(lens.max()))
+
+
+def cpu_baseline(pf, dc):
+    """Time the oracle on the host on a bounded sample: 128 evenly spaced prefill query
+    rows (all heads) and 8 of the 32 decode sequences."""
+    import numpy as np
+    from oracle import oracle
+
+    threads = oracle.max_threads()
+    S, Hq, Hkv, d = pf["S"], pf["Hq"], pf["Hkv"], pf["d"]
+    q = pf["q"].float().cpu().numpy()
+    k = pf["k"].float().cpu().numpy()
+    v = pf["v"].float().cpu().numpy()
+    rows = np.linspace(0, S - 1, 128).astype(np.int64)
+    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=rows[:4], nthreads=threads)  # warm
+    t0 = time.perf_counter()
+    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=rows, nthreads=threads)
+    t_pf = time.perf_counter() - t0
+    flops = float(sum(4.0 * d * Hq * (r + 1) for r in rows))
+
+    nseq = 8
+    kp = dc["kp"][0].float().cpu().numpy()
+    vp = dc["vp"][0].float().cpu().numpy()
+    qd = dc["q"][:nseq].float().cpu().numpy()
+    bt = dc["bt"][:nseq].cpu().numpy()
+    lens = dc["lens"][:nseq]
+    t0 = time.perf_counter()
+    oracle.decode_paged(qd, kp, vp, bt, lens, nthreads=threads)
+    t_dc = time.perf_counter() - t0
+    kv_bytes = 2 * int(lens.sum()) * Hkv * d * 2
+    return {
+        "value": flops / t_pf / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"causal prefill rows {len(rows)} of {S} (evenly spaced, all {Hq} heads), "
+                  f"fp32 oracle on fp16-valued inputs, OpenMP over rows; {t_pf:.2f} s",
+        "decode": {"value": kv_bytes / t_dc / 1e9, "unit": "GB/s",
+                   "sample": f"{nseq} of 32 paged-decode sequences; {t_dc:.2f} s"},
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(every box has one MI355X; see DESIGN.md for how the path shards)",
+              file=sys.stderr)
+        return 2
+    import torch
+    from orinmllm_amd import kernel as K
+
+    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC3)
+    pf = make_prefill(dtype, gen)
+    dc = make_decode(dtype, gen, args.pools)
+    ws_bytes = K.decode_workspace_size(dc["B"], dc["Hq"], dc["Hkv"], dc["d"], dc["maxlen"])
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def prefill():
+        K.flash_attention_prefill_cu(0, pf["S"], pf["Hq"], pf["Hkv"], pf["d"], pf["Hq"] // pf["Hkv"],
+                                     0, pf["S"], pf["Hkv"] * pf["d"], pf["q"], pf["o"], pf["k"],
+                                     pf["v"])
+
+    def decode(i):
+        p = i % args.pools
+        K.paged_decode_cu(dc["q"], dc["kp"][p], dc["vp"][p], dc["o"], dc["bt"], dc["lens_d"],
+                          dc["maxlen"], workspace=ws)
+
+    for i in range(args.warmup):
+        prefill()
+        decode(i)
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        e = ev[i]
+        e[0].record(stream)
+        prefill()
+        e[1].record(stream)
+        e[2].record(stream)
+        decode(args.warmup + i)
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    pf_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    dc_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    pf_tflops = pf["flops"] / (pf_ms * 1e-3) / 1e12
+    dc_gbs = dc["kv_bytes"] / (dc_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": "attn prefill TFLOP/s + decode KV GB/s (Qwen3-8B GQA fp16), 1 MI355X",
+        "value": round(pf_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.dtype == "fp16" else "bf16",
+        "data": "synthetic (seeded N(0,1); Q/K RMSNorm+RoPE)",
+        "config": {
+            "workload": "C3 causal GQA prefill S=4096 Hq=32 Hkv=8 d=128 + C4 paged decode "
+                        "B=32 Hq=32 Hkv=8 d=128 L~U[512,4096] block 16",
+            "prefill_ms": round(pf_ms, 4),
+            "decode_ms": round(dc_ms, 4),
+            "kv_pools_rotated": args.pools,
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": round(pf_tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(pf_tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "decode": {
+            "metric": "paged decode KV-read GB/s", "value": round(dc_gbs, 1), "unit": "GB/s",
+            "kv_bytes_per_call": dc["kv_bytes"],
+            "roofline": {"bound": "hbm", "achieved": round(dc_gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(dc_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": None},
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(pf, dc)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

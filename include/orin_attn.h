@@ -1,0 +1,213 @@
+/*
+ * orin_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Each entry point replaces one function of OrinMLLM's attention path
+ * (paths relative to the OrinMLLM source tree) with the same argument meaning,
+ * flattened to plain pointers: tensor::Tensor arguments become device pointers,
+ * CudaConfig* becomes the stream the kernels are queued on (a hipStream_t,
+ * NULL = the default stream), and the element type is an explicit code.
+ *
+ * Conventions shared by every entry point:
+ *  - dim = head_num*head_size, kv_dim = kv_head_num*head_size; query head h reads
+ *    kv head h / kv_mul (kuiper/source/op/kernels/cpu/mha_kernel.cpp:29).
+ *  - KV caches are kuiper's [layers, max_seq_len, kv_dim]; the layer is selected
+ *    with layer_index * max_seq_len * kv_dim, as the reference wrappers do.
+ *  - softmax scale is 1/sqrt(head_size) unless an entry point takes `scale`
+ *    (0 there also means 1/sqrt(head_size)).
+ *  - Everything is asynchronous on `stream`; nothing synchronises the host.
+ *  - The return value is ORIN_OK or a negative ORIN_ERR_* code.  Argument errors
+ *    are detected before anything is queued.  The reference layers return
+ *    base::error::InvalidArgument for non-positive sizes
+ *    (kuiper/source/op/flash_attention.cpp:32-37) and do not check launches; the
+ *    adapter maps ORIN_ERR_INVALID_ARG to InvalidArgument and the rest to
+ *    InternalError.
+ *  - Output may alias query (prefill is called with output == query by
+ *    kuiper/source/model/qwen3_vl.cpp:2871-2878): every workgroup reads its own
+ *    query rows before it writes the same rows.
+ */
+#ifndef ORIN_ATTN_H
+#define ORIN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types: values follow base::DataType (kuiper/include/base/base.h:58-64),
+ * which has fp32 = 1 and fp16 = 4; bf16 is new. */
+#define ORIN_DTYPE_FP32 1
+#define ORIN_DTYPE_FP16 4
+#define ORIN_DTYPE_BF16 5
+
+#define ORIN_OK 0
+#define ORIN_ERR_INVALID_ARG (-1) /* non-positive size, null pointer, inconsistent heads */
+#define ORIN_ERR_UNSUPPORTED (-2) /* dtype / head_size / block_size this build has no kernel for */
+#define ORIN_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+#define ORIN_ERR_LAUNCH (-4)      /* the HIP runtime rejected a launch or allocation */
+
+#define ORIN_ATTN_ABI_VERSION 1
+
+int orin_attn_abi_version(void);
+const char* orin_attn_status_string(int status);
+/* Text of the last HIP error seen by this library in this thread ("" if none). */
+const char* orin_attn_last_hip_error(void);
+
+/* ------------------------------------------------------------------ decode (fp32 MHA) */
+
+/*
+ * kernel::mha_kernel_cu (kuiper/source/op/kernels/cuda/mha_kernel.cuh:4-8; the
+ * MHAKernel typedef of kernels_interface.h:24-30, obtained from get_mha_kernel,
+ * kernels_interfaces.cpp:63-72).  fp32.  Query position `pos` attends to cache rows
+ * 0..pos of layer `layer_index`.  `seq_len` is the cache capacity (max_seq_len).
+ * `score` is the caller's [head_num, seq_len] fp32 scratch (kScoreStorage): it is
+ * used as split-KV workspace and its contents afterwards are unspecified.
+ */
+int orin_mha_kernel(int32_t pos, int32_t head_num, int32_t layer_index, int32_t seq_len,
+                    int32_t kv_dim, int32_t kv_mul, int32_t head_size, float* mha_out,
+                    const float* query, float* score, const float* key_cache,
+                    const float* value_cache, void* stream);
+
+/*
+ * kernel::mha_kernel_cu_gpu_pos (mha_kernel.cuh:13-19): as orin_mha_kernel with the
+ * position read from device memory, so the launch can be captured into a HIP graph
+ * and replayed while *pos_ptr changes.  The launch shape depends only on seq_len.
+ */
+int orin_mha_kernel_gpu_pos(const int32_t* pos_ptr, int32_t head_num, int32_t layer_index,
+                            int32_t seq_len, int32_t kv_dim, int32_t kv_mul, int32_t head_size,
+                            float* mha_out, const float* query, float* score,
+                            const float* key_cache, const float* value_cache, void* stream);
+
+/*
+ * kernel::batched_mha_kernel_cu (mha_kernel.cuh:21-26): fp32 causal prefill of
+ * seq_len query rows [seq_len, dim] at positions start_pos..start_pos+seq_len-1;
+ * row i attends cache rows 0..start_pos+i.  `score` ([seq_len, head_num,
+ * max_seq_len] in the reference) is not needed and may be NULL.
+ */
+int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t layer_index,
+                     int32_t max_seq_len, int32_t dim, int32_t kv_dim, int32_t kv_mul,
+                     int32_t head_size, float* mha_out, const float* query, float* score,
+                     const float* key_cache, const float* value_cache, void* stream);
+
+/* ------------------------------------------------------------------ flash attention */
+
+/*
+ * kernel::flash_attention_prefill_cu / flash_attention_prefill_fp16_cu /
+ * flash_attention2_prefill_cu / flash_attention2_prefill_fp16_cu
+ * (kuiper/source/op/kernels/cuda/flash_attention_kernel.cuh:27-80, 143-181).
+ * Causal GQA prefill: query/output [seq_len, dim], caches [layers, max_seq_len, kv_dim];
+ * row i attends 0..start_pos+i (flash_attention_kernel.cu:575-578).  dtype selects the
+ * reference's fp32 or fp16 variant; bf16 is new.  fp16/bf16 run on MFMA.
+ */
+int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
+                                 int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                                 int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                                 const void* query, void* output, const void* key_cache,
+                                 const void* value_cache, int32_t dtype, void* stream);
+
+/*
+ * kernel::flash_attention_decode_cu / flash_attention_decode_fp16_cu /
+ * flash_attention2_decode_cu / flash_attention2_decode_fp16_cu
+ * (flash_attention_kernel.cuh:50-63, 84-97, 186-216).  One query row [dim] at
+ * position pos over cache rows 0..pos.  Split-KV partials go to a workspace owned
+ * by this library (grown on demand per device; see orin_attn_workspace_reserve).
+ */
+int orin_flash_attention_decode(int32_t pos, int32_t head_num, int32_t kv_head_num,
+                                int32_t head_size, int32_t kv_mul, int32_t layer_index,
+                                int32_t max_seq_len, int32_t kv_dim, const void* query,
+                                void* output, const void* key_cache, const void* value_cache,
+                                int32_t dtype, void* stream);
+
+/*
+ * kernel::flash_attention_decode_fp16_gpu_pos_cu / flash_attention2_decode_fp16_gpu_pos_cu
+ * (flash_attention_kernel.cuh:103-117, 222-234): the decode above with the position
+ * read from device memory (HIP-graph capturable).  The launch shape and workspace
+ * depend only on max_seq_len; reserve the workspace before capturing.
+ */
+int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num,
+                                        int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                                        int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                                        const void* query, void* output, const void* key_cache,
+                                        const void* value_cache, int32_t dtype, void* stream);
+
+/* Bytes of library-owned workspace the flash decode entry points need for a cache
+ * of max_seq_len rows, and a call that allocates it on the current device now (so
+ * that a later graph capture does not allocate). */
+size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head_size,
+                                                  int32_t max_seq_len);
+int orin_attn_workspace_reserve(size_t bytes);
+
+/* ------------------------------------------------------------------ batched decode */
+
+/*
+ * Batched decode over per-sequence contiguous caches.  No reference function: the
+ * reference decodes one sequence (kuiper/source/model/qwen_base.cpp:675-781); this is
+ * that decode applied to `batch` rows.  query/out [batch, head_num*head_size];
+ * sequence b's token t, kv head g lives at
+ *   cache + b*cache_batch_stride + t*cache_tok_stride + g*head_size   (elements).
+ * context_lens (device, [batch]) gives each row's KV length; max_context_len bounds
+ * them (it sets the launch shape).  split_tokens: tokens per split (multiple of 64),
+ * 0 = automatic.  Workspace: orin_attn_decode_workspace_size bytes (may be NULL when
+ * that is 0).
+ */
+size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t kv_head_num,
+                                       int32_t head_size, int32_t max_context_len,
+                                       int32_t split_tokens);
+int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t kv_head_num,
+                                      int32_t max_context_len, int32_t split_tokens);
+int orin_attn_decode(const void* query, const void* key_cache, const void* value_cache,
+                     void* out, int32_t batch, int32_t head_num, int32_t kv_head_num,
+                     int32_t head_size, int64_t cache_batch_stride, int64_t cache_tok_stride,
+                     const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
+                     float scale, int32_t split_tokens, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Paged batched decode.  No reference function (the reference has no block-table
+ * KV cache).  Pools are [num_blocks, block_size, kv_head_num, head_size]: block b of
+ * the pool holds block_size consecutive tokens in kuiper's per-token kv_dim layout.
+ * Sequence s's token t lives in pool block block_tables[s*max_blocks_per_seq +
+ * t/block_size], row t % block_size.  block_size must be a power of two.  For equal
+ * split_tokens the result is bit-identical to orin_attn_decode on a contiguous copy
+ * of the same KV.
+ */
+int orin_attn_decode_paged(const void* query, const void* k_pool, const void* v_pool, void* out,
+                           int32_t batch, int32_t head_num, int32_t kv_head_num,
+                           int32_t head_size, const int32_t* block_tables,
+                           int32_t max_blocks_per_seq, int32_t block_size,
+                           const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
+                           float scale, int32_t split_tokens, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ vision */
+
+/*
+ * kernel::vision_attention_pretransposed_cu
+ * (kuiper/source/op/kernels/cuda/vision_encoder_kernel.cuh:159-170): bidirectional
+ * attention of num_tokens tokens over q/k/v [num_heads, num_tokens, head_dim] into
+ * output [num_tokens, num_heads*head_dim].  The reference's out_transposed and scores
+ * workspaces are not needed and may be NULL.  fp16 / bf16 (MFMA) or fp32.
+ */
+int orin_vision_attention_pretransposed(const void* q, const void* k, const void* v,
+                                        void* output, void* out_transposed, void* scores,
+                                        int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                        float softmax_scale, int32_t dtype, void* stream);
+
+/*
+ * Varlen form: tokens are packed segments (images) given by cu_seqlens (device,
+ * n_seqs+1 entries, cu_seqlens[0] = 0, cu_seqlens[n_seqs] = num_tokens); every token
+ * attends to all tokens of its own segment.  No reference function (the reference
+ * builds cu_seqlens, kuiper/source/model/qwen3_vl.cpp:1561-1568, but attends over one
+ * segment).  max_seqlen bounds the segment lengths.
+ */
+int orin_vision_attention_varlen(const void* q, const void* k, const void* v, void* output,
+                                 const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                                 int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                 float softmax_scale, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORIN_ATTN_H */

@@ -1,0 +1,551 @@
+// extern "C" entry points of liborin_attn.so (declared in include/orin_attn.h).
+// Argument checking, the per-call launch shape (split-KV sizing) and the
+// library-owned decode workspace live here; the kernels are in decode.hip and fwd.hip.
+#include <math.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+#include "orin_attn.h"
+
+using namespace orin;
+
+namespace {
+
+thread_local std::string g_last_hip_error;
+
+int hip_status(hipError_t e) {
+  if (e == hipSuccess) return ORIN_OK;
+  g_last_hip_error = hipGetErrorString(e);
+  return ORIN_ERR_LAUNCH;
+}
+
+float resolve_scale(float scale, int head_size) {
+  return scale > 0.f ? scale : 1.0f / sqrtf((float)head_size);
+}
+
+int round_up(long x, int m) { return (int)((x + m - 1) / m * m); }
+
+// Tokens per split for a decode launch with `base_blocks` (row, kv head, head group)
+// units and rows of up to max_len tokens.  Aims at ~2048 workgroups (8 per CU) with
+// at least 256 tokens (one 64-token tile per wave) per split.
+int auto_split_tokens(long base_blocks, int max_len) {
+  if (max_len <= 0) return 256;
+  const long target = 2048;
+  long splits = (target + base_blocks - 1) / base_blocks;
+  if (splits < 1) splits = 1;
+  int st = round_up((max_len + splits - 1) / splits, 64);
+  if (st < 256) st = 256;
+  if (st >= max_len) st = round_up(max_len, 64);
+  return st;
+}
+
+long decode_base_blocks(int rows, int head_num, int kv_head_num) {
+  const int kv_mul = head_num / kv_head_num;
+  return (long)rows * kv_head_num * (kv_mul / decode_heads_per_block(kv_mul));
+}
+
+int n_splits(int max_len, int split_tokens) {
+  return max_len <= 0 ? 1 : (max_len + split_tokens - 1) / split_tokens;
+}
+
+size_t ws_bytes(int rows, int head_num, int head_size, int splits) {
+  return splits <= 1 ? 0 : (size_t)rows * head_num * splits * (head_size + 2) * sizeof(float);
+}
+
+bool heads_ok(int head_num, int kv_head_num, int kv_mul) {
+  return head_num > 0 && kv_head_num > 0 && kv_mul > 0 && head_num == kv_head_num * kv_mul;
+}
+
+// Library-owned workspace, one grow-only buffer per device.
+std::mutex g_ws_mu;
+std::vector<std::pair<void*, size_t>> g_ws;
+
+int library_workspace(size_t bytes, void** out) {
+  *out = nullptr;
+  if (bytes == 0) return ORIN_OK;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
+  auto& slot = g_ws[dev];
+  if (slot.second < bytes) {
+    if (slot.first) {
+      // Earlier launches may still read the old buffer.
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_status(e);
+      (void)hipFree(slot.first);
+      slot = {nullptr, 0};
+    }
+    void* p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return hip_status(e);
+    slot = {p, bytes};
+  }
+  *out = slot.first;
+  return ORIN_OK;
+}
+
+DecodeArgs decode_defaults() {
+  DecodeArgs a = {};
+  a.max_splits = 1;
+  a.split_tokens = 1 << 30;
+  return a;
+}
+
+// Split size for a kuiper single-sequence decode whose workspace must fit in
+// cap_bytes (0 = unlimited).
+int kuiper_decode_split(int head_num, int kv_head_num, int head_size, int max_len,
+                        size_t cap_bytes, bool capped) {
+  int st = auto_split_tokens(decode_base_blocks(1, head_num, kv_head_num), max_len);
+  while (capped && n_splits(max_len, st) > 1 &&
+         ws_bytes(1, head_num, head_size, n_splits(max_len, st)) > cap_bytes)
+    st *= 2;
+  return st;
+}
+
+// max_len: the longest row the launch must cover (0 = rows are single-split by
+// construction).  Rows are clamped to max_splits * split_tokens tokens.
+int run_decode(DecodeArgs& a, int dtype, int max_len, hipStream_t stream) {
+  a.max_splits = n_splits(max_len, a.split_tokens);
+  if (a.max_splits <= 1) a.max_splits = 1;
+  a.len_cap = max_len > 0 ? max_len : (1 << 30);
+  return hip_status(launch_decode(a, dtype, stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int orin_attn_abi_version(void) { return ORIN_ATTN_ABI_VERSION; }
+
+const char* orin_attn_status_string(int status) {
+  switch (status) {
+    case ORIN_OK: return "ok";
+    case ORIN_ERR_INVALID_ARG: return "invalid argument";
+    case ORIN_ERR_UNSUPPORTED: return "unsupported dtype/head_size/block_size";
+    case ORIN_ERR_WORKSPACE: return "workspace missing or too small";
+    case ORIN_ERR_LAUNCH: return "HIP launch or allocation error";
+  }
+  return "unknown status";
+}
+
+const char* orin_attn_last_hip_error(void) { return g_last_hip_error.c_str(); }
+
+int orin_attn_workspace_reserve(size_t bytes) {
+  void* p;
+  return library_workspace(bytes, &p);
+}
+
+// ------------------------------------------------------------------ fp32 MHA
+
+static int mha_common(int32_t pos, const int32_t* pos_ptr, int32_t head_num, int32_t layer_index,
+                      int32_t seq_len, int32_t kv_dim, int32_t kv_mul, int32_t head_size,
+                      float* mha_out, const float* query, float* score, const float* key_cache,
+                      const float* value_cache, void* stream) {
+  if (head_size <= 0 || seq_len <= 0 || kv_dim <= 0 || layer_index < 0 || kv_dim % head_size)
+    return ORIN_ERR_INVALID_ARG;
+  const int kv_head_num = kv_dim / head_size;
+  if (!heads_ok(head_num, kv_head_num, kv_mul)) return ORIN_ERR_INVALID_ARG;
+  if (!mha_out || !query || !key_cache || !value_cache) return ORIN_ERR_INVALID_ARG;
+  if (!pos_ptr && (pos < 0 || pos >= seq_len)) return ORIN_ERR_INVALID_ARG;
+  if (!decode_supports(kF32, head_size)) return ORIN_ERR_UNSUPPORTED;
+  const size_t cap = score ? (size_t)head_num * seq_len * sizeof(float) : 0;
+  // Host position: size the split for pos+1 keys; device position: for the capacity.
+  const int max_len = pos_ptr ? seq_len : pos + 1;
+  DecodeArgs a = decode_defaults();
+  a.split_tokens = kuiper_decode_split(head_num, kv_head_num, head_size, max_len, cap, true);
+  const long layer_off = (long)layer_index * seq_len * kv_dim;
+  a.q = query;
+  a.q_row_stride = (long)head_num * head_size;
+  a.q_head_stride = head_size;
+  a.k = key_cache + layer_off;
+  a.v = value_cache + layer_off;
+  a.kv_tok_stride = kv_dim;
+  a.kv_head_stride = head_size;
+  if (pos_ptr) {
+    a.lens = pos_ptr;
+    a.len_add = 1;
+  } else {
+    a.len_base = pos + 1;
+  }
+  a.o = mha_out;
+  a.o_row_stride = (long)head_num * head_size;
+  a.o_head_stride = head_size;
+  a.ws = score;
+  a.n_rows = 1;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = kv_mul;
+  a.head_size = head_size;
+  a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  if (n_splits(max_len, a.split_tokens) > 1 && !score) return ORIN_ERR_WORKSPACE;
+  return run_decode(a, kF32, max_len, (hipStream_t)stream);
+}
+
+int orin_mha_kernel(int32_t pos, int32_t head_num, int32_t layer_index, int32_t seq_len,
+                    int32_t kv_dim, int32_t kv_mul, int32_t head_size, float* mha_out,
+                    const float* query, float* score, const float* key_cache,
+                    const float* value_cache, void* stream) {
+  return mha_common(pos, nullptr, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size,
+                    mha_out, query, score, key_cache, value_cache, stream);
+}
+
+int orin_mha_kernel_gpu_pos(const int32_t* pos_ptr, int32_t head_num, int32_t layer_index,
+                            int32_t seq_len, int32_t kv_dim, int32_t kv_mul, int32_t head_size,
+                            float* mha_out, const float* query, float* score,
+                            const float* key_cache, const float* value_cache, void* stream) {
+  if (!pos_ptr) return ORIN_ERR_INVALID_ARG;
+  return mha_common(0, pos_ptr, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size,
+                    mha_out, query, score, key_cache, value_cache, stream);
+}
+
+// Causal prefill on the per-row kernel (fp32, or any dtype the MFMA path lacks).
+static int prefill_rows(int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t kv_head_num,
+                        int32_t head_size, int32_t kv_mul, const void* query, void* output,
+                        const void* k, const void* v, int32_t kv_dim, int dtype,
+                        hipStream_t stream) {
+  DecodeArgs a = decode_defaults();
+  a.q = query;
+  a.q_row_stride = (long)head_num * head_size;
+  a.q_head_stride = head_size;
+  a.k = k;
+  a.v = v;
+  a.kv_tok_stride = kv_dim;
+  a.kv_head_stride = head_size;
+  a.len_base = start_pos + 1;
+  a.len_step = 1;
+  a.o = output;
+  a.o_row_stride = (long)head_num * head_size;
+  a.o_head_stride = head_size;
+  a.n_rows = seq_len;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = kv_mul;
+  a.head_size = head_size;
+  a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  return run_decode(a, dtype, 0, stream);
+}
+
+int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t layer_index,
+                     int32_t max_seq_len, int32_t dim, int32_t kv_dim, int32_t kv_mul,
+                     int32_t head_size, float* mha_out, const float* query, float* score,
+                     const float* key_cache, const float* value_cache, void* stream) {
+  (void)score;
+  if (head_size <= 0 || seq_len <= 0 || max_seq_len <= 0 || kv_dim <= 0 || start_pos < 0 ||
+      layer_index < 0 || kv_dim % head_size || dim != head_num * head_size ||
+      start_pos + seq_len > max_seq_len)
+    return ORIN_ERR_INVALID_ARG;
+  const int kv_head_num = kv_dim / head_size;
+  if (!heads_ok(head_num, kv_head_num, kv_mul)) return ORIN_ERR_INVALID_ARG;
+  if (!mha_out || !query || !key_cache || !value_cache) return ORIN_ERR_INVALID_ARG;
+  if (!decode_supports(kF32, head_size)) return ORIN_ERR_UNSUPPORTED;
+  const long layer_off = (long)layer_index * max_seq_len * kv_dim;
+  return prefill_rows(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, query,
+                      mha_out, key_cache + layer_off, value_cache + layer_off, kv_dim, kF32,
+                      (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------ flash attention
+
+static size_t elem_size(int dtype) { return dtype == kF32 ? 4 : 2; }
+
+int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
+                                 int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                                 int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                                 const void* query, void* output, const void* key_cache,
+                                 const void* value_cache, int32_t dtype, void* stream) {
+  if (head_size <= 0 || seq_len <= 0 || max_seq_len <= 0 || start_pos < 0 || layer_index < 0 ||
+      kv_dim != kv_head_num * head_size || start_pos + seq_len > max_seq_len)
+    return ORIN_ERR_INVALID_ARG;
+  if (!heads_ok(head_num, kv_head_num, kv_mul)) return ORIN_ERR_INVALID_ARG;
+  if (!query || !output || !key_cache || !value_cache) return ORIN_ERR_INVALID_ARG;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return ORIN_ERR_UNSUPPORTED;
+  const size_t layer_off = (size_t)layer_index * max_seq_len * kv_dim * elem_size(dtype);
+  const char* k = static_cast<const char*>(key_cache) + layer_off;
+  const char* v = static_cast<const char*>(value_cache) + layer_off;
+  if (dtype == kF32) {
+    if (!decode_supports(kF32, head_size)) return ORIN_ERR_UNSUPPORTED;
+    return prefill_rows(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, query,
+                        output, k, v, kv_dim, kF32, (hipStream_t)stream);
+  }
+  if (!fwd_supports(dtype, head_size)) return ORIN_ERR_UNSUPPORTED;
+  FwdArgs a = {};
+  a.q = query;
+  a.q_tok_stride = (long)head_num * head_size;
+  a.q_head_stride = head_size;
+  a.k = k;
+  a.v = v;
+  a.kv_tok_stride = kv_dim;
+  a.kv_head_stride = head_size;
+  a.o = output;
+  a.o_tok_stride = (long)head_num * head_size;
+  a.o_head_stride = head_size;
+  a.n_q = seq_len;
+  a.start_pos = start_pos;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = kv_mul;
+  a.head_size = head_size;
+  a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  return hip_status(launch_fwd_causal(a, dtype, (hipStream_t)stream));
+}
+
+static int flash_decode_common(int32_t pos, const int32_t* pos_ptr, int32_t head_num,
+                               int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                               int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                               const void* query, void* output, const void* key_cache,
+                               const void* value_cache, int32_t dtype, void* stream) {
+  if (head_size <= 0 || max_seq_len <= 0 || layer_index < 0 || kv_dim != kv_head_num * head_size)
+    return ORIN_ERR_INVALID_ARG;
+  if (!heads_ok(head_num, kv_head_num, kv_mul)) return ORIN_ERR_INVALID_ARG;
+  if (!query || !output || !key_cache || !value_cache) return ORIN_ERR_INVALID_ARG;
+  if (!pos_ptr && (pos < 0 || pos >= max_seq_len)) return ORIN_ERR_INVALID_ARG;
+  if (!decode_supports(dtype, head_size)) return ORIN_ERR_UNSUPPORTED;
+  const int max_len = pos_ptr ? max_seq_len : pos + 1;
+  DecodeArgs a = decode_defaults();
+  a.split_tokens = kuiper_decode_split(head_num, kv_head_num, head_size, max_len, 0, false);
+  const int splits = n_splits(max_len, a.split_tokens);
+  void* ws = nullptr;
+  int st = library_workspace(ws_bytes(1, head_num, head_size, splits), &ws);
+  if (st != ORIN_OK) return st;
+  const size_t layer_off = (size_t)layer_index * max_seq_len * kv_dim * elem_size(dtype);
+  a.q = query;
+  a.q_row_stride = (long)head_num * head_size;
+  a.q_head_stride = head_size;
+  a.k = static_cast<const char*>(key_cache) + layer_off;
+  a.v = static_cast<const char*>(value_cache) + layer_off;
+  a.kv_tok_stride = kv_dim;
+  a.kv_head_stride = head_size;
+  if (pos_ptr) {
+    a.lens = pos_ptr;
+    a.len_add = 1;
+  } else {
+    a.len_base = pos + 1;
+  }
+  a.o = output;
+  a.o_row_stride = (long)head_num * head_size;
+  a.o_head_stride = head_size;
+  a.ws = static_cast<float*>(ws);
+  a.n_rows = 1;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = kv_mul;
+  a.head_size = head_size;
+  a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  return run_decode(a, dtype, max_len, (hipStream_t)stream);
+}
+
+int orin_flash_attention_decode(int32_t pos, int32_t head_num, int32_t kv_head_num,
+                                int32_t head_size, int32_t kv_mul, int32_t layer_index,
+                                int32_t max_seq_len, int32_t kv_dim, const void* query,
+                                void* output, const void* key_cache, const void* value_cache,
+                                int32_t dtype, void* stream) {
+  return flash_decode_common(pos, nullptr, head_num, kv_head_num, head_size, kv_mul, layer_index,
+                             max_seq_len, kv_dim, query, output, key_cache, value_cache, dtype,
+                             stream);
+}
+
+int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num,
+                                        int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                                        int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                                        const void* query, void* output, const void* key_cache,
+                                        const void* value_cache, int32_t dtype, void* stream) {
+  if (!pos_ptr) return ORIN_ERR_INVALID_ARG;
+  return flash_decode_common(0, pos_ptr, head_num, kv_head_num, head_size, kv_mul, layer_index,
+                             max_seq_len, kv_dim, query, output, key_cache, value_cache, dtype,
+                             stream);
+}
+
+size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head_size,
+                                                  int32_t max_seq_len) {
+  if (head_num <= 0 || head_size <= 0 || max_seq_len <= 0) return 0;
+  // Worst case over kv_head_num: the split size shrinks as the unit count drops,
+  // so size for kv_head_num = 1.
+  const int st = auto_split_tokens(decode_base_blocks(1, 1, 1), max_seq_len);
+  return ws_bytes(1, head_num, head_size, n_splits(max_seq_len, st));
+}
+
+// ------------------------------------------------------------------ batched decode
+
+int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t kv_head_num,
+                                      int32_t max_context_len, int32_t split_tokens) {
+  if (split_tokens > 0) return split_tokens;
+  if (batch <= 0 || kv_head_num <= 0 || head_num % kv_head_num) return 0;
+  return auto_split_tokens(decode_base_blocks(batch, head_num, kv_head_num), max_context_len);
+}
+
+size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t kv_head_num,
+                                       int32_t head_size, int32_t max_context_len,
+                                       int32_t split_tokens) {
+  const int st =
+      orin_attn_decode_split_tokens(batch, head_num, kv_head_num, max_context_len, split_tokens);
+  if (st <= 0 || head_size <= 0) return 0;
+  return ws_bytes(batch, head_num, head_size, n_splits(max_context_len, st));
+}
+
+static int batched_decode(const void* query, const void* k, const void* v, void* out,
+                          int32_t batch, int32_t head_num, int32_t kv_head_num, int32_t head_size,
+                          int64_t batch_stride, int64_t tok_stride, const int32_t* block_tables,
+                          int32_t max_blocks, int32_t block_size, const int32_t* context_lens,
+                          int32_t max_context_len, int32_t dtype, float scale,
+                          int32_t split_tokens, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (batch <= 0 || head_size <= 0 || max_context_len < 0 || split_tokens < 0 ||
+      kv_head_num <= 0 || head_num <= 0 || head_num % kv_head_num)
+    return ORIN_ERR_INVALID_ARG;
+  if (!query || !k || !v || !out || !context_lens) return ORIN_ERR_INVALID_ARG;
+  if (!decode_supports(dtype, head_size)) return ORIN_ERR_UNSUPPORTED;
+  int bs_log2 = 0;
+  if (block_tables) {
+    if (block_size <= 0 || max_blocks <= 0 || (long)max_blocks * block_size < max_context_len)
+      return ORIN_ERR_INVALID_ARG;
+    if (block_size & (block_size - 1)) return ORIN_ERR_UNSUPPORTED;
+    while ((1 << bs_log2) < block_size) ++bs_log2;
+  }
+  const int st =
+      orin_attn_decode_split_tokens(batch, head_num, kv_head_num, max_context_len, split_tokens);
+  const size_t need = ws_bytes(batch, head_num, head_size, n_splits(max_context_len, st));
+  if (need > 0 && (!workspace || workspace_bytes < need)) return ORIN_ERR_WORKSPACE;
+  DecodeArgs a = decode_defaults();
+  a.split_tokens = st;
+  a.q = query;
+  a.q_row_stride = (long)head_num * head_size;
+  a.q_head_stride = head_size;
+  a.k = k;
+  a.v = v;
+  a.kv_tok_stride = tok_stride;
+  a.kv_head_stride = head_size;
+  a.kv_row_stride = batch_stride;
+  a.block_table = block_tables;
+  a.bt_row_stride = max_blocks;
+  a.bs_log2 = bs_log2;
+  a.lens = context_lens;
+  a.o = out;
+  a.o_row_stride = (long)head_num * head_size;
+  a.o_head_stride = head_size;
+  a.ws = static_cast<float*>(workspace);
+  a.n_rows = batch;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = head_num / kv_head_num;
+  a.head_size = head_size;
+  a.scale_log2 = resolve_scale(scale, head_size) * kLog2e;
+  return run_decode(a, dtype, max_context_len, (hipStream_t)stream);
+}
+
+int orin_attn_decode(const void* query, const void* key_cache, const void* value_cache,
+                     void* out, int32_t batch, int32_t head_num, int32_t kv_head_num,
+                     int32_t head_size, int64_t cache_batch_stride, int64_t cache_tok_stride,
+                     const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
+                     float scale, int32_t split_tokens, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (cache_tok_stride < (int64_t)kv_head_num * head_size || cache_batch_stride < 0)
+    return ORIN_ERR_INVALID_ARG;
+  return batched_decode(query, key_cache, value_cache, out, batch, head_num, kv_head_num,
+                        head_size, cache_batch_stride, cache_tok_stride, nullptr, 0, 0,
+                        context_lens, max_context_len, dtype, scale, split_tokens, workspace,
+                        workspace_bytes, stream);
+}
+
+int orin_attn_decode_paged(const void* query, const void* k_pool, const void* v_pool, void* out,
+                           int32_t batch, int32_t head_num, int32_t kv_head_num,
+                           int32_t head_size, const int32_t* block_tables,
+                           int32_t max_blocks_per_seq, int32_t block_size,
+                           const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
+                           float scale, int32_t split_tokens, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!block_tables) return ORIN_ERR_INVALID_ARG;
+  return batched_decode(query, k_pool, v_pool, out, batch, head_num, kv_head_num, head_size, 0,
+                        (int64_t)kv_head_num * head_size, block_tables, max_blocks_per_seq,
+                        block_size, context_lens, max_context_len, dtype, scale, split_tokens,
+                        workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------ vision
+
+static int vision_common(const void* q, const void* k, const void* v, void* output,
+                         const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                         int32_t num_tokens, int32_t num_heads, int32_t head_dim, float scale,
+                         int32_t dtype, void* stream) {
+  if (num_tokens <= 0 || num_heads <= 0 || head_dim <= 0 || !q || !k || !v || !output)
+    return ORIN_ERR_INVALID_ARG;
+  if (cu_seqlens && (n_seqs <= 0 || max_seqlen <= 0)) return ORIN_ERR_INVALID_ARG;
+  const float sl2 = resolve_scale(scale, head_dim) * kLog2e;
+  const long tok = head_dim, hs = (long)num_tokens * head_dim;
+  if (dtype == kF16 || dtype == kBF16) {
+    if (!fwd_supports(dtype, head_dim)) return ORIN_ERR_UNSUPPORTED;
+    FwdArgs a = {};
+    a.q = q;
+    a.q_tok_stride = tok;
+    a.q_head_stride = hs;
+    a.k = k;
+    a.v = v;
+    a.kv_tok_stride = tok;
+    a.kv_head_stride = hs;
+    a.o = output;
+    a.o_tok_stride = (long)num_heads * head_dim;
+    a.o_head_stride = head_dim;
+    a.n_q = num_tokens;
+    a.cu_seqlens = cu_seqlens;
+    a.n_seg = cu_seqlens ? n_seqs : 1;
+    a.max_seqlen = cu_seqlens ? max_seqlen : num_tokens;
+    a.Hq = num_heads;
+    a.Hkv = num_heads;
+    a.kv_mul = 1;
+    a.head_size = head_dim;
+    a.scale_log2 = sl2;
+    return hip_status(launch_fwd_varlen(a, dtype, (hipStream_t)stream));
+  }
+  if (dtype != kF32) return ORIN_ERR_UNSUPPORTED;
+  if (!decode_supports(kF32, head_dim)) return ORIN_ERR_UNSUPPORTED;
+  DecodeArgs a = decode_defaults();
+  a.q = q;
+  a.q_row_stride = tok;
+  a.q_head_stride = hs;
+  a.k = k;
+  a.v = v;
+  a.kv_tok_stride = tok;
+  a.kv_head_stride = hs;
+  if (cu_seqlens) {
+    a.cu_seqlens = cu_seqlens;
+    a.n_seg = n_seqs;
+  } else {
+    a.len_base = num_tokens;
+  }
+  a.o = output;
+  a.o_row_stride = (long)num_heads * head_dim;
+  a.o_head_stride = head_dim;
+  a.n_rows = num_tokens;
+  a.Hq = num_heads;
+  a.Hkv = num_heads;
+  a.kv_mul = 1;
+  a.head_size = head_dim;
+  a.scale_log2 = sl2;
+  return run_decode(a, kF32, 0, (hipStream_t)stream);
+}
+
+int orin_vision_attention_pretransposed(const void* q, const void* k, const void* v,
+                                        void* output, void* out_transposed, void* scores,
+                                        int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                        float softmax_scale, int32_t dtype, void* stream) {
+  (void)out_transposed;
+  (void)scores;
+  return vision_common(q, k, v, output, nullptr, 1, num_tokens, num_tokens, num_heads, head_dim,
+                       softmax_scale, dtype, stream);
+}
+
+int orin_vision_attention_varlen(const void* q, const void* k, const void* v, void* output,
+                                 const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                                 int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+                                 float softmax_scale, int32_t dtype, void* stream) {
+  if (!cu_seqlens) return ORIN_ERR_INVALID_ARG;
+  return vision_common(q, k, v, output, cu_seqlens, n_seqs, max_seqlen, num_tokens, num_heads,
+                       head_dim, softmax_scale, dtype, stream);
+}
+
+}  // extern "C"

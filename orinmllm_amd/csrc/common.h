@@ -1,0 +1,152 @@
+// Shared device helpers for the gfx950 attention kernels: element types, 16-byte
+// vectors, wave-level reductions built on DPP and ds_bpermute, and exp2.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace orin {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// Hardware base-2 exponential (v_exp_f32).  exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------- 16-byte lane chunk
+// A lane chunk is 16 bytes of one K or V row: 8 halves or 4 floats.
+template <typename T>
+struct Chunk {
+  static constexpr int kElems = 16 / sizeof(T);
+  u32x4 raw;
+};
+
+// Dot product of two 16-byte chunks, accumulated in fp32 onto acc.
+// fp16/bf16 use v_dot2_f32_{f16,bf16}: the products of two 16-bit floats are
+// exact in fp32, only the additions round.
+// Chunks are reinterpreted as whole vectors only: this toolchain mis-lowers
+// __builtin_bit_cast applied to a single element of an ext_vector (it yields
+// element 0 for every index).
+__device__ __forceinline__ float chunk_dot(const Chunk<f16>& a, const Chunk<f16>& b,
+                                           float acc) {
+  const f16x8 x = __builtin_bit_cast(f16x8, a.raw), y = __builtin_bit_cast(f16x8, b.raw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2(f16x2{x[2 * i], x[2 * i + 1]},
+                                 f16x2{y[2 * i], y[2 * i + 1]}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float chunk_dot(const Chunk<bf16>& a, const Chunk<bf16>& b,
+                                           float acc) {
+  const bf16x8 x = __builtin_bit_cast(bf16x8, a.raw), y = __builtin_bit_cast(bf16x8, b.raw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{x[2 * i], x[2 * i + 1]},
+                                          bf16x2{y[2 * i], y[2 * i + 1]}, acc,
+                                          false);
+  return acc;
+}
+__device__ __forceinline__ float chunk_dot(const Chunk<float>& a, const Chunk<float>& b,
+                                           float acc) {
+  const f32x4 x = __builtin_bit_cast(f32x4, a.raw), y = __builtin_bit_cast(f32x4, b.raw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(x[i], y[i], acc);
+  return acc;
+}
+
+// Unpack a chunk into fp32 values.
+__device__ __forceinline__ void chunk_unpack(const Chunk<f16>& c, float* out) {
+  const f16x8 x = __builtin_bit_cast(f16x8, c.raw);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (float)x[i];
+}
+__device__ __forceinline__ void chunk_unpack(const Chunk<bf16>& c, float* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bf16 -> fp32 is a 16-bit shift of the bit pattern.
+    const uint32_t w = c.raw[i];
+    out[2 * i] = __uint_as_float(w << 16);
+    out[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void chunk_unpack(const Chunk<float>& c, float* out) {
+  const f32x4 x = __builtin_bit_cast(f32x4, c.raw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = x[i];
+}
+
+template <typename T>
+__device__ __forceinline__ Chunk<T> load_chunk(const T* p) {
+  Chunk<T> c;
+  c.raw = *reinterpret_cast<const u32x4*>(p);
+  return c;
+}
+
+// ---------------------------------------------------------------- wave reductions
+// DPP controls (CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
+constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i+8) mod 16 inside a row
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float sum8(float x) {
+  x += dpp_mov<kDppQuadXor1>(x);
+  x += dpp_mov<kDppQuadXor2>(x);
+  x += dpp_mov<kDppHalfMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float shfl_xor_f(float x, int mask) {
+  int lane = __lane_id();
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
+}
+
+// Max / sum across the 8 lane groups of a wave (lanes with equal lane%8).
+__device__ __forceinline__ float max_across_groups8(float x) {
+  x = fmaxf(x, dpp_mov<kDppRowRor8>(x));
+  x = fmaxf(x, shfl_xor_f(x, 16));
+  x = fmaxf(x, shfl_xor_f(x, 32));
+  return x;
+}
+__device__ __forceinline__ float sum_across_groups8(float x) {
+  x += dpp_mov<kDppRowRor8>(x);
+  x += shfl_xor_f(x, 16);
+  x += shfl_xor_f(x, 32);
+  return x;
+}
+
+}  // namespace orin

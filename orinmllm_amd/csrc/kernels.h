@@ -1,0 +1,62 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace orin {
+
+// Element type codes; values follow base::DataType (kuiper/include/base/base.h:58-64)
+// with bf16 added.
+enum { kF32 = 1, kF16 = 4, kBF16 = 5 };
+
+// Decode / per-row attention.  Row r attends to tokens [0, len(r)) of its own
+// KV sequence.  All strides are in elements.
+struct DecodeArgs {
+  const void* q;  // q(r, h, j) = q[r*q_row_stride + h*q_head_stride + j]
+  long q_row_stride, q_head_stride;
+  const void* k;  // k(r, t, g, j) = k[map_r(t) + g*kv_head_stride + j]
+  const void* v;
+  long kv_tok_stride, kv_head_stride, kv_row_stride;
+  const int* block_table;  // paged: map_r(t) = (bt[r][t>>bs_log2] << bs_log2 | t&mask) * tok_stride
+  long bt_row_stride;
+  int bs_log2;
+  const int* lens;  // len(r) = lens[r] + len_add  if lens
+  int len_add;
+  int len_base, len_step;  // len(r) = len_base + r*len_step otherwise
+  int len_cap;             // len(r) is clamped to len_cap (the launch was sized for it)
+  const int* cu_seqlens;   // varlen: rows are tokens; row r attends its segment
+  int n_seg;
+  void* o;  // o(r, h, j) = o[r*o_row_stride + h*o_head_stride + j]
+  long o_row_stride, o_head_stride;
+  float* ws;  // [n_rows, Hq, max_splits, head_size + 2] fp32 partials (unused if max_splits == 1)
+  int max_splits, split_tokens;
+  int n_rows, Hq, Hkv, kv_mul, head_size;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+int decode_heads_per_block(int kv_mul);
+bool decode_supports(int dtype, int head_size);
+hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t stream);
+
+// Tile-parallel attention forward on MFMA (fp16 / bf16): causal prefill over a
+// kuiper-layout cache, or bidirectional varlen segments.
+struct FwdArgs {
+  const void* q;  // q(t, h, j) = q[t*q_tok_stride + h*q_head_stride + j]
+  long q_tok_stride, q_head_stride;
+  const void* k;  // k(t, g, j) = k[t*kv_tok_stride + g*kv_head_stride + j]
+  const void* v;
+  long kv_tok_stride, kv_head_stride;
+  void* o;
+  long o_tok_stride, o_head_stride;
+  int n_q;        // query rows (causal: seq_len; varlen: total tokens)
+  int start_pos;  // causal: query i sits at position start_pos + i
+  const int* cu_seqlens;  // varlen (device), n_seg + 1 entries; null = one segment of n_q
+  int n_seg, max_seqlen;
+  int Hq, Hkv, kv_mul, head_size;
+  float scale_log2;
+};
+
+bool fwd_supports(int dtype, int head_size);
+hipError_t launch_fwd_causal(const FwdArgs& a, int dtype, hipStream_t stream);
+hipError_t launch_fwd_varlen(const FwdArgs& a, int dtype, hipStream_t stream);
+
+}  // namespace orin

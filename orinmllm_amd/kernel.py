@@ -1,0 +1,292 @@
+"""Host mirror of OrinMLLM's ``namespace kernel`` attention entry points.
+
+Every function keeps the name and argument order of the reference function it
+replaces (paths relative to the OrinMLLM source tree) and calls the HIP library
+through the C ABI.  ``tensor::Tensor`` arguments are torch tensors on the GPU
+(PyTorch only provides device memory and the stream here); ``CudaConfig*`` is a
+:class:`CudaConfig` carrying the stream.  The element type comes from the tensors.
+
+Errors raise :class:`orinmllm_amd._lib.OrinAttnError`; nothing falls back to a CPU
+implementation.
+"""
+from __future__ import annotations
+
+import enum
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+class DeviceType(enum.IntEnum):
+    """base::DeviceType (kuiper/include/base/base.h:50-54)."""
+    kDeviceUnknown = 0
+    kDeviceCPU = 1
+    kDeviceCUDA = 2
+
+
+class DataType(enum.IntEnum):
+    """base::DataType (kuiper/include/base/base.h:58-64) plus bf16."""
+    kDataTypeUnknown = 0
+    kDataTypeFp32 = 1
+    kDataTypeInt8 = 2
+    kDataTypeInt32 = 3
+    kDataTypeFp16 = 4
+    kDataTypeBf16 = 5
+
+
+class AttentionType(enum.IntEnum):
+    """base::AttentionType (kuiper/include/base/base.h:113-118)."""
+    kAttentionMHA = 0
+    kAttentionFlash1 = 1
+    kAttentionFlash2 = 2
+
+
+_TORCH_DTYPE = {
+    torch.float32: _lib.DTYPE_FP32,
+    torch.float16: _lib.DTYPE_FP16,
+    torch.bfloat16: _lib.DTYPE_BF16,
+}
+
+
+@dataclass
+class CudaConfig:
+    """kernel::CudaConfig (kuiper/include/base/cuda_config.h:17-33): the stream the
+    kernels are queued on.  None = torch's current stream."""
+    stream: Optional[torch.cuda.Stream] = None
+
+
+def _stream(config: Optional[CudaConfig]) -> int:
+    s = config.stream if config is not None and config.stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor], name: str) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the attention kernels have no CPU path)")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _dtype(*ts: torch.Tensor) -> int:
+    dt = ts[0].dtype
+    for t in ts[1:]:
+        if t.dtype != dt:
+            raise ValueError(f"mixed dtypes {dt} and {t.dtype}")
+    if dt not in _TORCH_DTYPE:
+        raise ValueError(f"unsupported dtype {dt}")
+    return _TORCH_DTYPE[dt]
+
+
+def _i32(t: torch.Tensor, name: str) -> int:
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32")
+    return _ptr(t, name)
+
+
+# ---------------------------------------------------------------- fp32 MHA
+
+def mha_kernel_cu(pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size, mha_out,
+                  query_tensor, score_tensor, key_cache_tensor, value_cache_tensor,
+                  device_type=DeviceType.kDeviceCUDA, config=None):
+    """kernel::mha_kernel_cu (kuiper/source/op/kernels/cuda/mha_kernel.cuh:4-8)."""
+    if _dtype(mha_out, query_tensor, key_cache_tensor, value_cache_tensor) != _lib.DTYPE_FP32:
+        raise ValueError("mha_kernel_cu is fp32")
+    _lib.check("orin_mha_kernel", _lib.load().orin_mha_kernel(
+        pos, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size,
+        _ptr(mha_out, "mha_out"), _ptr(query_tensor, "query"), _ptr(score_tensor, "score"),
+        _ptr(key_cache_tensor, "key_cache"), _ptr(value_cache_tensor, "value_cache"),
+        _stream(config)))
+
+
+def mha_kernel_cu_gpu_pos(pos_ptr, head_num, layer_index, seq_len, kv_dim, kv_mul, head_size,
+                          mha_out, query_tensor, score_tensor, key_cache_tensor,
+                          value_cache_tensor, device_type=DeviceType.kDeviceCUDA, config=None):
+    """kernel::mha_kernel_cu_gpu_pos (mha_kernel.cuh:13-19); pos_ptr: int32 GPU tensor [1]."""
+    _lib.check("orin_mha_kernel_gpu_pos", _lib.load().orin_mha_kernel_gpu_pos(
+        _i32(pos_ptr, "pos_ptr"), head_num, layer_index, seq_len, kv_dim, kv_mul, head_size,
+        _ptr(mha_out, "mha_out"), _ptr(query_tensor, "query"), _ptr(score_tensor, "score"),
+        _ptr(key_cache_tensor, "key_cache"), _ptr(value_cache_tensor, "value_cache"),
+        _stream(config)))
+
+
+def batched_mha_kernel_cu(start_pos, seq_len, head_num, layer_index, max_seq_len, dim, kv_dim,
+                          kv_mul, head_size, mha_out, query_tensor, score_tensor,
+                          key_cache_tensor, value_cache_tensor,
+                          device_type=DeviceType.kDeviceCUDA, config=None):
+    """kernel::batched_mha_kernel_cu (mha_kernel.cuh:21-26)."""
+    _lib.check("orin_batched_mha", _lib.load().orin_batched_mha(
+        start_pos, seq_len, head_num, layer_index, max_seq_len, dim, kv_dim, kv_mul, head_size,
+        _ptr(mha_out, "mha_out"), _ptr(query_tensor, "query"), _ptr(score_tensor, "score"),
+        _ptr(key_cache_tensor, "key_cache"), _ptr(value_cache_tensor, "value_cache"),
+        _stream(config)))
+
+
+def get_mha_kernel(device_type):
+    """kernel::get_mha_kernel (kuiper/source/op/kernels/kernels_interfaces.cpp:63-72).
+
+    Only the GPU kernel is provided: the reference's CPU kernel is not part of this
+    library (it is restated under oracle/ as a test checker only)."""
+    if DeviceType(device_type) == DeviceType.kDeviceCUDA:
+        return mha_kernel_cu
+    raise NotImplementedError(f"no MHA kernel for {DeviceType(device_type).name} in this library")
+
+
+# ---------------------------------------------------------------- flash attention
+
+def _prefill(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, layer_index,
+             max_seq_len, kv_dim, query, output, key_cache, value_cache, config):
+    dt = _dtype(query, output, key_cache, value_cache)
+    _lib.check("orin_flash_attention_prefill", _lib.load().orin_flash_attention_prefill(
+        start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, layer_index, max_seq_len,
+        kv_dim, _ptr(query, "query"), _ptr(output, "output"), _ptr(key_cache, "key_cache"),
+        _ptr(value_cache, "value_cache"), dt, _stream(config)))
+
+
+def flash_attention_prefill_cu(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul,
+                               layer_index, max_seq_len, kv_dim, query, output, key_cache,
+                               value_cache, config=None):
+    """kernel::flash_attention_prefill_cu (flash_attention_kernel.cuh:27-42) and its fp16 /
+    FlashAttention-2 siblings: the element type is taken from the tensors."""
+    _prefill(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, layer_index,
+             max_seq_len, kv_dim, query, output, key_cache, value_cache, config)
+
+
+flash_attention_prefill_fp16_cu = flash_attention_prefill_cu
+flash_attention2_prefill_cu = flash_attention_prefill_cu
+flash_attention2_prefill_fp16_cu = flash_attention_prefill_cu
+
+
+def flash_attention_decode_cu(pos, head_num, kv_head_num, head_size, kv_mul, layer_index,
+                              max_seq_len, kv_dim, query, output, key_cache, value_cache,
+                              config=None):
+    """kernel::flash_attention_decode_cu (flash_attention_kernel.cuh:50-63) and its fp16 /
+    FlashAttention-2 siblings."""
+    dt = _dtype(query, output, key_cache, value_cache)
+    _lib.check("orin_flash_attention_decode", _lib.load().orin_flash_attention_decode(
+        pos, head_num, kv_head_num, head_size, kv_mul, layer_index, max_seq_len, kv_dim,
+        _ptr(query, "query"), _ptr(output, "output"), _ptr(key_cache, "key_cache"),
+        _ptr(value_cache, "value_cache"), dt, _stream(config)))
+
+
+flash_attention_decode_fp16_cu = flash_attention_decode_cu
+flash_attention2_decode_cu = flash_attention_decode_cu
+flash_attention2_decode_fp16_cu = flash_attention_decode_cu
+
+
+def flash_attention_decode_fp16_gpu_pos_cu(pos_ptr, head_num, kv_head_num, head_size, kv_mul,
+                                           layer_index, max_seq_len, kv_dim, query, output,
+                                           key_cache, value_cache, config=None):
+    """kernel::flash_attention_decode_fp16_gpu_pos_cu (flash_attention_kernel.cuh:103-117)."""
+    dt = _dtype(query, output, key_cache, value_cache)
+    _lib.check("orin_flash_attention_decode_gpu_pos",
+               _lib.load().orin_flash_attention_decode_gpu_pos(
+                   _i32(pos_ptr, "pos_ptr"), head_num, kv_head_num, head_size, kv_mul,
+                   layer_index, max_seq_len, kv_dim, _ptr(query, "query"),
+                   _ptr(output, "output"), _ptr(key_cache, "key_cache"),
+                   _ptr(value_cache, "value_cache"), dt, _stream(config)))
+
+
+flash_attention2_decode_fp16_gpu_pos_cu = flash_attention_decode_fp16_gpu_pos_cu
+
+
+def reserve_decode_workspace(head_num, head_size, max_seq_len):
+    """Allocate the library-owned flash-decode workspace now (before a graph capture)."""
+    lib = _lib.load()
+    n = lib.orin_flash_attention_decode_workspace_size(head_num, head_size, max_seq_len)
+    _lib.check("orin_attn_workspace_reserve", lib.orin_attn_workspace_reserve(n))
+
+
+# ---------------------------------------------------------------- batched / paged decode
+
+def decode_workspace_size(batch, head_num, kv_head_num, head_size, max_context_len,
+                          split_tokens=0):
+    return int(_lib.load().orin_attn_decode_workspace_size(
+        batch, head_num, kv_head_num, head_size, max_context_len, split_tokens))
+
+
+def _workspace(nbytes, workspace, device):
+    if nbytes == 0:
+        return None, 0
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace needs {nbytes} bytes")
+    return _ptr(workspace, "workspace"), workspace.numel() * workspace.element_size()
+
+
+def batched_decode_cu(query, key_cache, value_cache, out, context_lens, max_context_len,
+                      kv_head_num, cache_batch_stride=None, cache_tok_stride=None, scale=0.0,
+                      split_tokens=0, workspace=None, config=None):
+    """Decode one query row per sequence over per-sequence contiguous caches.
+
+    query/out [B, head_num, head_size]; caches [B, max_seq, kv_head_num, head_size]
+    unless explicit element strides are given; context_lens int32 [B] on the GPU."""
+    B, head_num, head_size = query.shape
+    if cache_tok_stride is None:
+        cache_tok_stride = kv_head_num * head_size
+    if cache_batch_stride is None:
+        cache_batch_stride = key_cache.stride(0)
+    dt = _dtype(query, key_cache, value_cache, out)
+    nbytes = decode_workspace_size(B, head_num, kv_head_num, head_size, max_context_len,
+                                   split_tokens)
+    wp, wn = _workspace(nbytes, workspace, query.device)
+    _lib.check("orin_attn_decode", _lib.load().orin_attn_decode(
+        _ptr(query, "query"), _ptr(key_cache, "key_cache"), _ptr(value_cache, "value_cache"),
+        _ptr(out, "out"), B, head_num, kv_head_num, head_size, cache_batch_stride,
+        cache_tok_stride, _i32(context_lens, "context_lens"), max_context_len, dt, scale,
+        split_tokens, wp, wn, _stream(config)))
+
+
+def paged_decode_cu(query, k_pool, v_pool, out, block_tables, context_lens, max_context_len,
+                    scale=0.0, split_tokens=0, workspace=None, config=None):
+    """Paged decode.  query/out [B, head_num, head_size]; pools
+    [num_blocks, block_size, kv_head_num, head_size]; block_tables int32 [B, max_blocks];
+    context_lens int32 [B]."""
+    B, head_num, head_size = query.shape
+    _, block_size, kv_head_num, hs2 = k_pool.shape
+    if hs2 != head_size:
+        raise ValueError("pool head_size differs from query head_size")
+    dt = _dtype(query, k_pool, v_pool, out)
+    nbytes = decode_workspace_size(B, head_num, kv_head_num, head_size, max_context_len,
+                                   split_tokens)
+    wp, wn = _workspace(nbytes, workspace, query.device)
+    _lib.check("orin_attn_decode_paged", _lib.load().orin_attn_decode_paged(
+        _ptr(query, "query"), _ptr(k_pool, "k_pool"), _ptr(v_pool, "v_pool"), _ptr(out, "out"),
+        B, head_num, kv_head_num, head_size, _i32(block_tables, "block_tables"),
+        block_tables.shape[1], block_size, _i32(context_lens, "context_lens"), max_context_len,
+        dt, scale, split_tokens, wp, wn, _stream(config)))
+
+
+# ---------------------------------------------------------------- vision
+
+def vision_attention_pretransposed_cu(q_trans, k_trans, v_trans, output, out_transposed, scores,
+                                      num_tokens, num_heads, head_dim, softmax_scale,
+                                      config=None):
+    """kernel::vision_attention_pretransposed_cu
+    (kuiper/source/op/kernels/cuda/vision_encoder_kernel.cuh:159-170)."""
+    dt = _dtype(q_trans, k_trans, v_trans, output)
+    _lib.check("orin_vision_attention_pretransposed",
+               _lib.load().orin_vision_attention_pretransposed(
+                   _ptr(q_trans, "q"), _ptr(k_trans, "k"), _ptr(v_trans, "v"),
+                   _ptr(output, "output"), _ptr(out_transposed, "out_transposed"),
+                   _ptr(scores, "scores"), num_tokens, num_heads, head_dim,
+                   float(softmax_scale), dt, _stream(config)))
+
+
+def vision_attention_varlen_cu(q_trans, k_trans, v_trans, output, cu_seqlens, max_seqlen,
+                               num_heads, head_dim, softmax_scale=0.0, config=None):
+    """Varlen vision attention: q/k/v [num_heads, N, head_dim], output [N, num_heads*head_dim],
+    cu_seqlens int32 [n_seqs+1] on the GPU."""
+    dt = _dtype(q_trans, k_trans, v_trans, output)
+    n_seqs = cu_seqlens.numel() - 1
+    num_tokens = q_trans.shape[1]
+    _lib.check("orin_vision_attention_varlen", _lib.load().orin_vision_attention_varlen(
+        _ptr(q_trans, "q"), _ptr(k_trans, "k"), _ptr(v_trans, "v"), _ptr(output, "output"),
+        _i32(cu_seqlens, "cu_seqlens"), n_seqs, max_seqlen, num_tokens, num_heads, head_dim,
+        float(softmax_scale), dt, _stream(config)))
