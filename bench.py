@@ -69,7 +69,7 @@ def make_prefill(dtype, gen):
     return dict(S=S, Hq=Hq, Hkv=Hkv, d=d, q=q, k=k, v=v, o=o, flops=flops)
 
 
-def make_decode(dtype, gen, pools):
+def make_decode(dtype, gen, pools, layout=1):
     import numpy as np
     import torch
     B, Hq, Hkv, d, bs = 32, 32, 8, 128, 16
@@ -84,14 +84,13 @@ def make_decode(dtype, gen, pools):
     for b in range(B):
         bt[b, : nblk[b]] = perm[off: off + nblk[b]]
         off += nblk[b]
-    kp = [torch.randn(total, bs, Hkv, d, device="cuda", generator=gen).to(dtype)
-          for _ in range(pools)]
-    vp = [torch.randn(total, bs, Hkv, d, device="cuda", generator=gen).to(dtype)
-          for _ in range(pools)]
+    shape = (total, bs, Hkv, d) if layout == 0 else (total, Hkv, bs, d)
+    kp = [torch.randn(*shape, device="cuda", generator=gen).to(dtype) for _ in range(pools)]
+    vp = [torch.randn(*shape, device="cuda", generator=gen).to(dtype) for _ in range(pools)]
     q = torch.randn(B, Hq, d, device="cuda", generator=gen).to(dtype)
     o = torch.empty_like(q)
     kv_bytes = 2 * int(lens.sum()) * Hkv * d * 2  # K and V, read once per kv head
-    return dict(B=B, Hq=Hq, Hkv=Hkv, d=d, bs=bs, lens=lens, lens_d=torch.from_numpy(lens).cuda(),
+    return dict(B=B, Hq=Hq, Hkv=Hkv, d=d, bs=bs, lens=lens, layout=layout, lens_d=torch.from_numpy(lens).cuda(),
                 bt=torch.from_numpy(bt).cuda(), kp=kp, vp=vp, q=q, o=o, kv_bytes=kv_bytes,
                 maxlen=int(lens.max()))
 
@@ -117,6 +116,9 @@ def cpu_baseline(pf, dc):
     nseq = 8
     kp = dc["kp"][0].float().cpu().numpy()
     vp = dc["vp"][0].float().cpu().numpy()
+    if dc["layout"] == 1:  # the oracle takes token-major pools
+        kp = np.ascontiguousarray(kp.transpose(0, 2, 1, 3))
+        vp = np.ascontiguousarray(vp.transpose(0, 2, 1, 3))
     qd = dc["q"][:nseq].float().cpu().numpy()
     bt = dc["bt"][:nseq].cpu().numpy()
     lens = dc["lens"][:nseq]
@@ -160,7 +162,7 @@ def main():
     def decode(i):
         p = i % args.pools
         K.paged_decode_cu(dc["q"], dc["kp"][p], dc["vp"][p], dc["o"], dc["bt"], dc["lens_d"],
-                          dc["maxlen"], workspace=ws)
+                          dc["maxlen"], workspace=ws, layout=dc["layout"])
 
     for i in range(args.warmup):
         prefill()

@@ -147,8 +147,8 @@ int orin_attn_workspace_reserve(size_t bytes);
  * sequence b's token t, kv head g lives at
  *   cache + b*cache_batch_stride + t*cache_tok_stride + g*head_size   (elements).
  * context_lens (device, [batch]) gives each row's KV length; max_context_len bounds
- * them (it sets the launch shape).  split_tokens: tokens per split (multiple of 64),
- * 0 = automatic.  Workspace: orin_attn_decode_workspace_size bytes (may be NULL when
+ * them (it sets the launch shape).  split_tokens: tokens per split (multiple of 64,
+ * else ORIN_ERR_INVALID_ARG), 0 = automatic.  Workspace: orin_attn_decode_workspace_size bytes (may be NULL when
  * that is 0).
  */
 size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t kv_head_num,
@@ -165,17 +165,24 @@ int orin_attn_decode(const void* query, const void* key_cache, const void* value
 
 /*
  * Paged batched decode.  No reference function (the reference has no block-table
- * KV cache).  Pools are [num_blocks, block_size, kv_head_num, head_size]: block b of
- * the pool holds block_size consecutive tokens in kuiper's per-token kv_dim layout.
+ * KV cache).  Block b of a pool holds block_size consecutive tokens of one sequence,
+ * for all kv heads, in one of two layouts:
+ *   ORIN_KV_LAYOUT_TOKEN_MAJOR  [num_blocks, block_size, kv_head_num, head_size]
+ *                               (each token row is kuiper's kv_dim layout)
+ *   ORIN_KV_LAYOUT_HEAD_MAJOR   [num_blocks, kv_head_num, block_size, head_size]
+ *                               (each (block, kv head) is one contiguous run)
  * Sequence s's token t lives in pool block block_tables[s*max_blocks_per_seq +
- * t/block_size], row t % block_size.  block_size must be a power of two.  For equal
+ * t/block_size], row t % block_size.  block_size must be a power of two >= 8
+ * (ORIN_ERR_UNSUPPORTED otherwise).  split_tokens must be a multiple of 64.  For equal
  * split_tokens the result is bit-identical to orin_attn_decode on a contiguous copy
- * of the same KV.
+ * of the same KV, in either layout.
  */
+#define ORIN_KV_LAYOUT_TOKEN_MAJOR 0
+#define ORIN_KV_LAYOUT_HEAD_MAJOR 1
 int orin_attn_decode_paged(const void* query, const void* k_pool, const void* v_pool, void* out,
                            int32_t batch, int32_t head_num, int32_t kv_head_num,
                            int32_t head_size, const int32_t* block_tables,
-                           int32_t max_blocks_per_seq, int32_t block_size,
+                           int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_layout,
                            const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
                            float scale, int32_t split_tokens, void* workspace,
                            size_t workspace_bytes, void* stream);

@@ -29,6 +29,9 @@ float resolve_scale(float scale, int head_size) {
 
 int round_up(long x, int m) { return (int)((x + m - 1) / m * m); }
 
+// The combine kernel merges at most this many splits per row.
+constexpr int kMaxSplits = 1024;
+
 // Tokens per split for a decode launch with `base_blocks` (row, kv head, head group)
 // units and rows of up to max_len tokens.  Aims at ~2048 workgroups (8 per CU) with
 // at least 256 tokens (one 64-token tile per wave) per split.
@@ -40,6 +43,7 @@ int auto_split_tokens(long base_blocks, int max_len) {
   int st = round_up((max_len + splits - 1) / splits, 64);
   if (st < 256) st = 256;
   if (st >= max_len) st = round_up(max_len, 64);
+  while ((max_len + st - 1) / st > kMaxSplits) st *= 2;
   return st;
 }
 
@@ -105,6 +109,7 @@ int kuiper_decode_split(int head_num, int kv_head_num, int head_size, int max_le
   while (capped && n_splits(max_len, st) > 1 &&
          ws_bytes(1, head_num, head_size, n_splits(max_len, st)) > cap_bytes)
     st *= 2;
+  while (n_splits(max_len, st) > kMaxSplits) st *= 2;
   return st;
 }
 
@@ -390,7 +395,8 @@ size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t 
 
 static int batched_decode(const void* query, const void* k, const void* v, void* out,
                           int32_t batch, int32_t head_num, int32_t kv_head_num, int32_t head_size,
-                          int64_t batch_stride, int64_t tok_stride, const int32_t* block_tables,
+                          int64_t batch_stride, int64_t tok_stride, int64_t head_stride,
+                          int64_t block_stride, const int32_t* block_tables,
                           int32_t max_blocks, int32_t block_size, const int32_t* context_lens,
                           int32_t max_context_len, int32_t dtype, float scale,
                           int32_t split_tokens, void* workspace, size_t workspace_bytes,
@@ -401,14 +407,17 @@ static int batched_decode(const void* query, const void* k, const void* v, void*
   if (!query || !k || !v || !out || !context_lens) return ORIN_ERR_INVALID_ARG;
   if (!decode_supports(dtype, head_size)) return ORIN_ERR_UNSUPPORTED;
   int bs_log2 = 0;
+  if (split_tokens % 64) return ORIN_ERR_INVALID_ARG;
   if (block_tables) {
     if (block_size <= 0 || max_blocks <= 0 || (long)max_blocks * block_size < max_context_len)
       return ORIN_ERR_INVALID_ARG;
-    if (block_size & (block_size - 1)) return ORIN_ERR_UNSUPPORTED;
+    // Each 8-token step of the kernel must lie inside one block.
+    if ((block_size & (block_size - 1)) || block_size < 8) return ORIN_ERR_UNSUPPORTED;
     while ((1 << bs_log2) < block_size) ++bs_log2;
   }
   const int st =
       orin_attn_decode_split_tokens(batch, head_num, kv_head_num, max_context_len, split_tokens);
+  if (n_splits(max_context_len, st) > kMaxSplits) return ORIN_ERR_INVALID_ARG;
   const size_t need = ws_bytes(batch, head_num, head_size, n_splits(max_context_len, st));
   if (need > 0 && (!workspace || workspace_bytes < need)) return ORIN_ERR_WORKSPACE;
   DecodeArgs a = decode_defaults();
@@ -419,9 +428,10 @@ static int batched_decode(const void* query, const void* k, const void* v, void*
   a.k = k;
   a.v = v;
   a.kv_tok_stride = tok_stride;
-  a.kv_head_stride = head_size;
+  a.kv_head_stride = head_stride;
   a.kv_row_stride = batch_stride;
   a.block_table = block_tables;
+  a.block_stride = block_stride;
   a.bt_row_stride = max_blocks;
   a.bs_log2 = bs_log2;
   a.lens = context_lens;
@@ -447,7 +457,7 @@ int orin_attn_decode(const void* query, const void* key_cache, const void* value
   if (cache_tok_stride < (int64_t)kv_head_num * head_size || cache_batch_stride < 0)
     return ORIN_ERR_INVALID_ARG;
   return batched_decode(query, key_cache, value_cache, out, batch, head_num, kv_head_num,
-                        head_size, cache_batch_stride, cache_tok_stride, nullptr, 0, 0,
+                        head_size, cache_batch_stride, cache_tok_stride, head_size, 0, nullptr, 0, 0,
                         context_lens, max_context_len, dtype, scale, split_tokens, workspace,
                         workspace_bytes, stream);
 }
@@ -455,13 +465,24 @@ int orin_attn_decode(const void* query, const void* key_cache, const void* value
 int orin_attn_decode_paged(const void* query, const void* k_pool, const void* v_pool, void* out,
                            int32_t batch, int32_t head_num, int32_t kv_head_num,
                            int32_t head_size, const int32_t* block_tables,
-                           int32_t max_blocks_per_seq, int32_t block_size,
+                           int32_t max_blocks_per_seq, int32_t block_size, int32_t kv_layout,
                            const int32_t* context_lens, int32_t max_context_len, int32_t dtype,
                            float scale, int32_t split_tokens, void* workspace,
                            size_t workspace_bytes, void* stream) {
-  if (!block_tables) return ORIN_ERR_INVALID_ARG;
+  if (!block_tables || block_size <= 0 || kv_head_num <= 0) return ORIN_ERR_INVALID_ARG;
+  const int64_t d = head_size, bs = block_size, hkv = kv_head_num;
+  int64_t tok_stride, head_stride;
+  if (kv_layout == ORIN_KV_LAYOUT_TOKEN_MAJOR) {
+    tok_stride = hkv * d;  // [num_blocks, block_size, kv_heads, head_size]
+    head_stride = d;
+  } else if (kv_layout == ORIN_KV_LAYOUT_HEAD_MAJOR) {
+    tok_stride = d;  // [num_blocks, kv_heads, block_size, head_size]
+    head_stride = bs * d;
+  } else {
+    return ORIN_ERR_INVALID_ARG;
+  }
   return batched_decode(query, k_pool, v_pool, out, batch, head_num, kv_head_num, head_size, 0,
-                        (int64_t)kv_head_num * head_size, block_tables, max_blocks_per_seq,
+                        tok_stride, head_stride, bs * hkv * d, block_tables, max_blocks_per_seq,
                         block_size, context_lens, max_context_len, dtype, scale, split_tokens,
                         workspace, workspace_bytes, stream);
 }

@@ -5,22 +5,28 @@
 //  flash_attention_kernel.cu:205-535 and :966-1175,
 //  flash_attention2_kernel.cu:409-816) with one design:
 //
-//  * A workgroup (4 waves) owns one (row, kv head, split): it reads that split's
-//    K/V once and serves the G query heads that share the kv head (GQA), so KV
+//  * A workgroup (4 waves) owns one (row, kv head, head group, split): it reads that
+//    split's K/V once and serves the G query heads that share the kv head (GQA), so KV
 //    bytes are read from HBM once per kv head instead of once per query head.
-//  * Inside a wave, 8 lanes own one token: lane k of the group loads the 16-byte
-//    chunks [128n + 16k, +16) of the token's K row (n < NV), so each load
-//    instruction covers 8 tokens x 128 contiguous bytes.  q.k is a per-lane
-//    dot2 followed by a 3-step DPP all-reduce over the 8 lanes.
-//  * Each wave keeps its own online-softmax state (running max m, partial sum l,
-//    accumulator acc) over 64-token tiles, so no barrier is needed per tile;
-//    the 4 waves are merged once through LDS at the end.
-//  * Splits are fixed-size ranges of logical token positions.  A row needing
-//    more than one split writes (acc, m, l) partials to the workspace and
-//    decode_combine merges them; a single-split row writes its output directly.
-//  * The address of token t is computed by one of three maps (contiguous cache,
-//    paged block table, varlen segment).  The arithmetic does not depend on the
-//    map, so paged and contiguous decode of the same KV are bit-identical.
+//  * Scores: 8 lanes own one token.  Lane k of the group loads the 16-byte chunks
+//    [128n + 16k, +16) of the token's K row (n < NV), so each load instruction covers
+//    8 tokens x 128 contiguous bytes; q.k is a per-lane dot2 followed by a 3-step DPP
+//    all-reduce over the 8 lanes.
+//  * Values: each lane owns D/64 consecutive output elements for every token.  A V row
+//    is one coalesced whole-wave load (D*sizeof(T)/64 bytes per lane) whose address is
+//    wave-uniform; each softmax weight is broadcast from the lane group that computed
+//    it with v_readlane (a scalar operand of the FMAs).  The accumulator is G * D/64 floats per lane and needs no
+//    cross-lane reduction at the end.
+//  * Each wave keeps its own online-softmax state over its tiles (no barrier per tile);
+//    the 4 waves are merged once through LDS.  Each wave software-pipelines its tiles:
+//    the next tile's K rows are requested once the current scores exist, its V rows
+//    once the current PV is done.
+//  * Splits are fixed-size ranges of logical token positions.  A row needing more than
+//    one split writes (acc, m, l) partials to the workspace and decode_combine merges
+//    them; a single-split row writes its output directly.
+//  * Token addresses come from a contiguous map (optionally per varlen segment) or a
+//    paged block table.  The arithmetic does not depend on the map, so paged and
+//    contiguous decode of the same KV are bit-identical.
 #include "common.h"
 #include "kernels.h"
 
@@ -30,43 +36,123 @@ namespace {
 
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
+constexpr int kMaxCombineSplits = 1024;  // the host sizes splits so a row has at most this many
 
 template <typename T, int D>
 struct DecodeShape {
   static constexpr int kRowBytes = D * (int)sizeof(T);
   static_assert(kRowBytes % 128 == 0, "head row must be a multiple of 128 bytes");
-  static constexpr int NV = kRowBytes / 128;           // 16-byte chunks per lane per token
-  static constexpr int VEC = 16 / (int)sizeof(T);      // elements per chunk
-  static constexpr int CH_STRIDE = 128 / (int)sizeof(T);  // elements between a lane's chunks
-  static constexpr int STEPS = (16 / NV) < 2 ? 2 : (16 / NV);  // 8-token groups per wave tile
-  static constexpr int TILE = STEPS * 8;               // tokens per wave tile
+  static constexpr int NV = kRowBytes / 128;              // K: 16-byte chunks per lane per token
+  static constexpr int VEC = 16 / (int)sizeof(T);         // K: elements per chunk
+  static constexpr int CH_STRIDE = 128 / (int)sizeof(T);  // K: elements between a lane's chunks
+  static constexpr int STEPS = (NV == 2) ? 2 : (NV == 1 ? 4 : (NV >= 8 ? 1 : 8 / NV));
+  static constexpr int TILE = STEPS * 8;                  // tokens per wave tile
+  static constexpr int EPL = D / kWave;                   // V: elements per lane
+  static constexpr int VB = EPL * (int)sizeof(T);         // V: bytes per lane per token
 };
 
-// Address of the K/V row of logical token `tok` of the current row, in elements,
-// relative to the k/v base pointer (kv head offset excluded).
+// Raw V fragment of one lane (VB bytes) and its conversion to fp32.
+template <int VB>
+struct VRaw;
+template <>
+struct VRaw<2> { typedef uint16_t type; };
+template <>
+struct VRaw<4> { typedef uint32_t type; };
+template <>
+struct VRaw<8> { typedef u32x2 type; };
+template <>
+struct VRaw<16> { typedef u32x4 type; };
+
+template <typename T, int EPL, typename R>
+__device__ __forceinline__ void v_unpack(const R& r, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    typedef float fv __attribute__((ext_vector_type(EPL)));
+    const fv x = __builtin_bit_cast(fv, r);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) out[i] = x[i];
+  } else if constexpr (EPL == 1) {
+    out[0] = (float)__builtin_bit_cast(T, r);
+  } else {
+    typedef T hv __attribute__((ext_vector_type(EPL)));
+    const hv x = __builtin_bit_cast(hv, r);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) out[i] = (float)x[i];
+  }
+}
+
+// Interleave two tokens' 16-bit V fragments: out[e] = (a.e, b.e) as a 16-bit pair.
+template <int EPL>
+__device__ __forceinline__ void pair_rows(uint16_t a, uint16_t b, uint32_t* out) {
+  out[0] = (uint32_t)a | ((uint32_t)b << 16);
+}
+template <int EPL>
+__device__ __forceinline__ void pair_rows(uint32_t a, uint32_t b, uint32_t* out) {
+  out[0] = __builtin_amdgcn_perm(b, a, 0x05040100u);  // (a.lo, b.lo)
+  out[1] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // (a.hi, b.hi)
+}
+template <int EPL>
+__device__ __forceinline__ void pair_rows(u32x2 a, u32x2 b, uint32_t* out) {
+  const uint32_t a0 = __builtin_bit_cast(u32x2, a).x, a1 = __builtin_bit_cast(u32x2, a).y;
+  const uint32_t b0 = __builtin_bit_cast(u32x2, b).x, b1 = __builtin_bit_cast(u32x2, b).y;
+  out[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+}
+
+// acc + p.x*v.x + p.y*v.y on 16-bit pairs (fp32 accumulate).
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t p, uint32_t v, float acc);
+template <>
+__device__ __forceinline__ float dot2<f16>(uint32_t p, uint32_t v, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), __builtin_bit_cast(f16x2, v), acc,
+                                false);
+}
+template <>
+__device__ __forceinline__ float dot2<bf16>(uint32_t p, uint32_t v, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
+                                         __builtin_bit_cast(bf16x2, v), acc, false);
+}
+
+// Address map of one row's KV sequence.  Offsets are in elements, relative to the
+// k/v base pointer (kv head offset excluded).  A token's row is
+//   contiguous: base + tok * tok_stride
+//   paged:      blk * block_stride + (tok % block_size) * tok_stride,
+//               blk = block_table[tok / block_size]
+// Paged: every 8-token K step (and every single V token) lies inside one block
+// (block_size >= 8, steps start at multiples of 8), so the block id is wave-uniform and
+// read with a scalar load, which does not wait on the vector loads in flight.
+template <bool PAGED>
 struct TokenMap {
-  int mode;           // 0 contiguous, 1 paged
   long base;          // contiguous: element offset of token 0 of this row
-  long tok_stride;    // elements between consecutive tokens (physical rows)
-  const int* bt_row;  // paged: this row's block table
+  long tok_stride;    // elements between consecutive token rows
+  long block_stride;  // paged: elements between consecutive pool blocks
+  const __attribute__((address_space(4))) int* bt_row;  // paged: this row's block table
   int bs_log2;
-  __device__ __forceinline__ long operator()(int tok) const {
-    if (mode == 1) {
-      long phys = ((long)bt_row[tok >> bs_log2] << bs_log2) + (tok & ((1 << bs_log2) - 1));
-      return phys * tok_stride;
-    }
-    return base + (long)tok * tok_stride;
+  __device__ __forceinline__ int block_of(int tok) const {
+    return PAGED ? bt_row[tok >> bs_log2] : 0;
+  }
+  // Element offset of the row of token `tok`, whose block id is `blk`.
+  __device__ __forceinline__ long row_offset(int tok, int blk) const {
+    if (PAGED)
+      return (long)blk * block_stride + (long)(tok & ((1 << bs_log2) - 1)) * tok_stride;
+    return (long)tok * tok_stride;
   }
 };
 
+__device__ __forceinline__ int find_segment(const int* cu, int n_seg, int row) {
+  int lo = 0, hi = n_seg - 1;  // s with cu[s] <= row < cu[s+1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= row) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 __device__ __forceinline__ int row_len_raw(const DecodeArgs& a, int row) {
   if (a.cu_seqlens) {
-    int lo = 0, hi = a.n_seg - 1;  // find s with cu[s] <= row < cu[s+1]
-    while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
-      if (a.cu_seqlens[mid] <= row) lo = mid; else hi = mid - 1;
-    }
-    return a.cu_seqlens[lo + 1] - a.cu_seqlens[lo];
+    const int s = find_segment(a.cu_seqlens, a.n_seg, row);
+    return a.cu_seqlens[s + 1] - a.cu_seqlens[s];
   }
   if (a.lens) return a.lens[row] + a.len_add;
   return a.len_base + row * a.len_step;
@@ -77,21 +163,24 @@ __device__ __forceinline__ int row_len(const DecodeArgs& a, int row) {
   return min(row_len_raw(a, row), a.len_cap);
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, bool PAGED>
 __global__ void __launch_bounds__(kDecodeThreads)
 decode_split_kernel(DecodeArgs a) {
   using S = DecodeShape<T, D>;
-  constexpr int NV = S::NV, VEC = S::VEC, STEPS = S::STEPS, TILE = S::TILE;
-  constexpr int EL = NV * VEC;  // fp32 accumulator elements per lane per head
+  constexpr int NV = S::NV, VEC = S::VEC, STEPS = S::STEPS, TILE = S::TILE, EPL = S::EPL;
+  typedef typename VRaw<S::VB>::type VR;
 
+  // Block order: kv head fastest, so the workgroups reading the Hkv interleaved head
+  // slices of the same token rows run together (DRAM row locality); then head group,
+  // split, row.
   const int n_hg = a.kv_mul / G;
   int bid = blockIdx.x;
-  const int split = bid % a.max_splits;
-  bid /= a.max_splits;
+  const int kvh = bid % a.Hkv;
+  bid /= a.Hkv;
   const int hg = bid % n_hg;
   bid /= n_hg;
-  const int kvh = bid % a.Hkv;
-  const int row = bid / a.Hkv;
+  const int split = bid % a.max_splits;
+  const int row = bid / a.max_splits;
 
   const int len = row_len(a, row);
   const int s0 = split * a.split_tokens;
@@ -108,36 +197,29 @@ decode_split_kernel(DecodeArgs a) {
   if (split >= nsplit) return;
   const int s1 = min(s0 + a.split_tokens, len);
 
-  TokenMap map;
-  if (a.block_table) {
-    map.mode = 1;
-    map.bt_row = a.block_table + (long)row * a.bt_row_stride;
-    map.bs_log2 = a.bs_log2;
-    map.base = 0;
-  } else {
-    map.mode = 0;
-    map.bt_row = nullptr;
-    map.bs_log2 = 0;
-    long base = (long)row * a.kv_row_stride;
-    if (a.cu_seqlens) {
-      int lo = 0, hi = a.n_seg - 1;
-      while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (a.cu_seqlens[mid] <= row) lo = mid; else hi = mid - 1;
-      }
-      base = (long)a.cu_seqlens[lo] * a.kv_tok_stride;
-    }
-    map.base = base;
-  }
+  TokenMap<PAGED> map;
   map.tok_stride = a.kv_tok_stride;
+  map.block_stride = a.block_stride;
+  map.bs_log2 = a.bs_log2;
+  map.bt_row = (const __attribute__((address_space(4))) int*)(
+      a.block_table + (PAGED ? (long)row * a.bt_row_stride : 0));
+  map.base = 0;
+  if (!PAGED) {
+    map.base = a.cu_seqlens
+                   ? (long)a.cu_seqlens[find_segment(a.cu_seqlens, a.n_seg, row)] * a.kv_tok_stride
+                   : (long)row * a.kv_row_stride;
+  }
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int k8 = lane & 7;   // chunk slot inside the token's row
-  const int grp = lane >> 3; // token group (0..7)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int k8 = lane & 7;    // K chunk slot inside the token's row
+  const int grp = lane >> 3;  // K token group (0..7)
 
-  const T* kb = reinterpret_cast<const T*>(a.k) + (long)kvh * a.kv_head_stride + k8 * VEC;
-  const T* vb = reinterpret_cast<const T*>(a.v) + (long)kvh * a.kv_head_stride + k8 * VEC;
+  // Wave-uniform bases; per-lane parts are 32-bit offsets added at the load.
+  const T* kb = reinterpret_cast<const T*>(a.k) + (long)kvh * a.kv_head_stride + map.base;
+  const T* vb = reinterpret_cast<const T*>(a.v) + (long)kvh * a.kv_head_stride + map.base;
+  const int k_lane = k8 * VEC;
+  const int v_lane = lane * EPL;
 
   // q chunks for the G heads, same element mapping as K.
   Chunk<T> qc[G][NV];
@@ -150,102 +232,169 @@ decode_split_kernel(DecodeArgs a) {
         qc[g][n] = load_chunk(qb + (long)(h0 + g) * a.q_head_stride + n * S::CH_STRIDE);
   }
 
-  float m[G], l[G], acc[G][EL];
+  float m[G], l[G], acc[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.f;
 #pragma unroll
-    for (int e = 0; e < EL; ++e) acc[g][e] = 0.f;
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
   }
 
   const float c = a.scale_log2;
-  for (int t0 = s0 + wave * TILE; t0 < s1; t0 += kDecodeWaves * TILE) {
-    Chunk<T> kc[STEPS][NV], vc[STEPS][NV];
-    bool valid[STEPS];
+  // Per-lane offsets (elements) inside an 8-token step, used when the whole tile lies
+  // below s1: K token group grp, V token r.
+  const int k_off = grp * (int)map.tok_stride + k_lane;
+  int v_off[8];
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      int tok = t0 + s * 8 + grp;
-      valid[s] = tok < s1;
-      long off = map(valid[s] ? tok : s1 - 1);
-#pragma unroll
-      for (int n = 0; n < NV; ++n) kc[s][n] = load_chunk(kb + off + n * S::CH_STRIDE);
-    }
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      int tok = t0 + s * 8 + grp;
-      long off = map(tok < s1 ? tok : s1 - 1);
-#pragma unroll
-      for (int n = 0; n < NV; ++n) vc[s][n] = load_chunk(vb + off + n * S::CH_STRIDE);
-    }
+  for (int r = 0; r < 8; ++r) v_off[r] = r * (int)map.tok_stride + v_lane;
 
-    float sc[STEPS][G];
+  // Block ids of the K steps / V tokens of the tile at t0.  In a tile that crosses s1,
+  // tokens >= s1 read row s1-1 (finite data; their weights are 0).
+  auto k_blocks = [&](int (&blk)[STEPS], int t0) {
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s)
+    for (int s = 0; s < STEPS; ++s) blk[s] = map.block_of(min(t0 + s * 8, s1 - 1));
+  };
+  auto load_k = [&](Chunk<T> (&dst)[STEPS][NV], int t0, const int (&blk)[STEPS]) {
+    const bool full = t0 + TILE <= s1;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
+    for (int s = 0; s < STEPS; ++s) {
+      const int step_tok = min(t0 + s * 8, s1 - 1);  // uniform
+      const T* rowp = kb + map.row_offset(step_tok, blk[s]);
+      const int lo = full ? k_off
+                          : (min(t0 + s * 8 + grp, s1 - 1) - step_tok) * (int)map.tok_stride +
+                                k_lane;
 #pragma unroll
-        for (int n = 0; n < NV; ++n) d = chunk_dot(qc[g][n], kc[s][n], d);
-        d = sum8(d);
-        sc[s][g] = valid[s] ? d * c : -INFINITY;
+      for (int n = 0; n < NV; ++n) dst[s][n] = load_chunk(rowp + lo + n * S::CH_STRIDE);
+    }
+  };
+  // V token j = 8s + r of the tile lies in the block of K step s; the step's row address
+  // is uniform.
+  auto load_v = [&](VR (&dst)[TILE], int t0, const int (&blk)[STEPS]) {
+    const bool full = t0 + TILE <= s1;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int step_tok = min(t0 + s * 8, s1 - 1);
+      const T* rowp = vb + map.row_offset(step_tok, blk[s]);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int off = full ? v_off[r]
+                             : (min(t0 + s * 8 + r, s1 - 1) - step_tok) * (int)map.tok_stride +
+                                   v_lane;
+        dst[s * 8 + r] = *reinterpret_cast<const VR*>(rowp + off);
       }
+    }
+  };
 
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float tm = sc[0][g];
-#pragma unroll
-      for (int s = 1; s < STEPS; ++s) tm = fmaxf(tm, sc[s][g]);
-      tm = max_across_groups8(tm);
-      const float mn = fmaxf(m[g], tm);
-      const float alpha = fast_exp2(m[g] - mn);
-      m[g] = mn;
-      float ls = 0.f;
+  int t0 = s0 + wave * TILE;
+  if (t0 < s1) {
+    Chunk<T> kc[STEPS][NV];
+    VR vr[TILE];
+    int blk[STEPS], nblk[STEPS];
+    k_blocks(blk, t0);
+    load_k(kc, t0, blk);
+    load_v(vr, t0, blk);
+    while (true) {
+      const int tn = t0 + kDecodeWaves * TILE;
+      const bool more = tn < s1;
+      if (more) k_blocks(nblk, tn);  // in flight while this tile's scores are computed
+
+      float sc[STEPS][G];
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) {
-        sc[s][g] = fast_exp2(sc[s][g] - mn);
-        ls += sc[s][g];
-      }
-      l[g] = l[g] * alpha + ls;
+        const bool valid = t0 + s * 8 + grp < s1;
 #pragma unroll
-      for (int e = 0; e < EL; ++e) acc[g][e] *= alpha;
-    }
+        for (int g = 0; g < G; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int n = 0; n < NV; ++n) d = chunk_dot(qc[g][n], kc[s][n], d);
+          d = sum8(d);
+          sc[s][g] = valid ? d * c : -INFINITY;
+        }
+      }
+      if (more) load_k(kc, tn, nblk);
 
+      float alpha[G];
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
+      for (int g = 0; g < G; ++g) {
+        float tm = sc[0][g];
 #pragma unroll
-      for (int n = 0; n < NV; ++n) {
-        float vf[VEC];
-        chunk_unpack(vc[s][n], vf);
+        for (int s = 1; s < STEPS; ++s) tm = fmaxf(tm, sc[s][g]);
+        tm = max_across_groups8(tm);
+        const float mn = fmaxf(m[g], tm);
+        alpha[g] = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        float ls = 0.f;
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int i = 0; i < VEC; ++i)
-            acc[g][n * VEC + i] = __builtin_fmaf(sc[s][g], vf[i], acc[g][n * VEC + i]);
+        for (int s = 0; s < STEPS; ++s) {
+          sc[s][g] = fast_exp2(sc[s][g] - mn);
+          ls += sc[s][g];
+        }
+        l[g] = l[g] * alpha[g] + ls;
       }
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha[g];
+      // Token j = 8s + r of the tile has its weights in lane group r (lane 8r); they are
+      // broadcast with v_readlane into scalar registers.
+      if constexpr (sizeof(T) == 2) {
+        // 16-bit K/V: tokens 8(2u)+r and 8(2u+1)+r share one packed weight pair, so one
+        // v_dot2 does two tokens.  The weights are rounded to T (as P is in the MFMA
+        // prefill); the normaliser l keeps the fp32 weights.
+        typedef T T2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int u = 0; u < STEPS / 2; ++u) {
+          uint32_t pw[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+            pw[g] = __builtin_bit_cast(uint32_t, T2{(T)sc[2 * u][g], (T)sc[2 * u + 1][g]});
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            uint32_t vp[EPL];
+            pair_rows<EPL>(vr[16 * u + r], vr[16 * u + 8 + r], vp);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const uint32_t p2 = __builtin_amdgcn_readlane(pw[g], r * 8);
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) acc[g][e] = dot2<T>(p2, vp[e], acc[g][e]);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < TILE; ++j) {
+          float vf[EPL];
+          v_unpack<T, EPL>(vr[j], vf);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float p = __builtin_bit_cast(
+                float,
+                __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[j >> 3][g]), (j & 7) * 8));
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(p, vf[e], acc[g][e]);
+          }
+        }
+      }
+      if (!more) break;
+      load_v(vr, tn, nblk);
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) blk[s] = nblk[s];
+      t0 = tn;
     }
   }
 
-  // Merge the 8 token groups of the wave (all groups share the wave's m).
+  // l: every lane of a token group holds the same partial sums; add the 8 groups.
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] = sum_across_groups8(l[g]);
-#pragma unroll
-    for (int e = 0; e < EL; ++e) acc[g][e] = sum_across_groups8(acc[g][e]);
-  }
+  for (int g = 0; g < G; ++g) l[g] = sum_across_groups8(l[g]);
 
-  // Merge the 4 waves through LDS: per wave [G][D] acc, then m, l.
+  // Merge the 4 waves through LDS.
   __shared__ float s_acc[kDecodeWaves][G][D];
   __shared__ float s_ml[kDecodeWaves][G][2];
-  if (grp == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int n = 0; n < NV; ++n)
-#pragma unroll
-        for (int i = 0; i < VEC; ++i)
-          s_acc[wave][g][n * S::CH_STRIDE + k8 * VEC + i] = acc[g][n * VEC + i];
-  }
+    for (int e = 0; e < EPL; ++e) s_acc[wave][g][lane * EPL + e] = acc[g][e];
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -282,34 +431,55 @@ decode_split_kernel(DecodeArgs a) {
 }
 
 // Merge split partials of every (row, head) whose row needed more than one split.
+// One wave per (row, head): lanes read the splits' (m, l) in parallel, the weights
+// exp2(m_s - M) / L go through LDS, then every lane forms D/64 outputs.
 template <typename T, int D>
 __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
+  constexpr int EPL = D / kWave;
   const int h = blockIdx.x % a.Hq;
   const int row = blockIdx.x / a.Hq;
   const int len = row_len(a, row);
   const int nsplit = len > 0 ? (len + a.split_tokens - 1) / a.split_tokens : 0;
   if (nsplit <= 1) return;
+  const int lane = threadIdx.x;
   const float* p = a.ws + ((long)row * a.Hq + h) * a.max_splits * (D + 2);
+  __shared__ float s_w[kMaxCombineSplits];
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p[s * (D + 2) + D]);
+  for (int s = lane; s < nsplit; s += kWave) M = fmaxf(M, p[s * (D + 2) + D]);
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) M = fmaxf(M, shfl_xor_f(M, mask));
   float L = 0.f;
-  for (int s = 0; s < nsplit; ++s)
-    L += fast_exp2(p[s * (D + 2) + D] - M) * p[s * (D + 2) + D + 1];
-  const float inv = 1.f / L;
-  T* out = reinterpret_cast<T*>(a.o) + (long)row * a.o_row_stride + (long)h * a.o_head_stride;
-  for (int dd = threadIdx.x; dd < D; dd += 64) {
-    float o = 0.f;
-    for (int s = 0; s < nsplit; ++s)
-      o += fast_exp2(p[s * (D + 2) + D] - M) * p[s * (D + 2) + dd];
-    out[dd] = from_f32<T>(o * inv);
+  for (int s = lane; s < nsplit; s += kWave) {
+    const float w = fast_exp2(p[s * (D + 2) + D] - M);
+    s_w[s] = w;
+    L += w * p[s * (D + 2) + D + 1];
   }
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) L += shfl_xor_f(L, mask);
+  __syncthreads();
+  const float inv = 1.f / L;
+  float o[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) o[e] = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float w = s_w[s];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = __builtin_fmaf(w, p[s * (D + 2) + lane * EPL + e], o[e]);
+  }
+  T* out = reinterpret_cast<T*>(a.o) + (long)row * a.o_row_stride + (long)h * a.o_head_stride;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) out[lane * EPL + e] = from_f32<T>(o[e] * inv);
 }
 
 template <typename T, int D, int G>
 hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_rows * a.Hkv * (a.kv_mul / G) * a.max_splits;
-  hipLaunchKernelGGL((decode_split_kernel<T, D, G>), dim3((unsigned)blocks), dim3(kDecodeThreads),
-                     0, stream, a);
+  if (a.block_table)
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, true>), dim3((unsigned)blocks),
+                       dim3(kDecodeThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, false>), dim3((unsigned)blocks),
+                       dim3(kDecodeThreads), 0, stream, a);
   if (a.max_splits > 1)
     hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.n_rows * a.Hq)), dim3(64),
                        0, stream, a);

@@ -16,8 +16,9 @@ struct DecodeArgs {
   const void* k;  // k(r, t, g, j) = k[map_r(t) + g*kv_head_stride + j]
   const void* v;
   long kv_tok_stride, kv_head_stride, kv_row_stride;
-  const int* block_table;  // paged: map_r(t) = (bt[r][t>>bs_log2] << bs_log2 | t&mask) * tok_stride
+  const int* block_table;  // paged: map_r(t) = bt[r][t>>bs_log2]*block_stride + (t&mask)*tok_stride
   long bt_row_stride;
+  long block_stride;
   int bs_log2;
   const int* lens;  // len(r) = lens[r] + len_add  if lens
   int len_add;

@@ -243,13 +243,22 @@ def batched_decode_cu(query, key_cache, value_cache, out, context_lens, max_cont
         split_tokens, wp, wn, _stream(config)))
 
 
+KV_LAYOUT_TOKEN_MAJOR = 0
+KV_LAYOUT_HEAD_MAJOR = 1
+
+
 def paged_decode_cu(query, k_pool, v_pool, out, block_tables, context_lens, max_context_len,
-                    scale=0.0, split_tokens=0, workspace=None, config=None):
+                    scale=0.0, split_tokens=0, workspace=None, config=None,
+                    layout=KV_LAYOUT_TOKEN_MAJOR):
     """Paged decode.  query/out [B, head_num, head_size]; pools
-    [num_blocks, block_size, kv_head_num, head_size]; block_tables int32 [B, max_blocks];
-    context_lens int32 [B]."""
+    [num_blocks, block_size, kv_head_num, head_size] (token-major) or
+    [num_blocks, kv_head_num, block_size, head_size] (head-major); block_tables int32
+    [B, max_blocks]; context_lens int32 [B]."""
     B, head_num, head_size = query.shape
-    _, block_size, kv_head_num, hs2 = k_pool.shape
+    if layout == KV_LAYOUT_TOKEN_MAJOR:
+        _, block_size, kv_head_num, hs2 = k_pool.shape
+    else:
+        _, kv_head_num, block_size, hs2 = k_pool.shape
     if hs2 != head_size:
         raise ValueError("pool head_size differs from query head_size")
     dt = _dtype(query, k_pool, v_pool, out)
@@ -259,7 +268,8 @@ def paged_decode_cu(query, k_pool, v_pool, out, block_tables, context_lens, max_
     _lib.check("orin_attn_decode_paged", _lib.load().orin_attn_decode_paged(
         _ptr(query, "query"), _ptr(k_pool, "k_pool"), _ptr(v_pool, "v_pool"), _ptr(out, "out"),
         B, head_num, kv_head_num, head_size, _i32(block_tables, "block_tables"),
-        block_tables.shape[1], block_size, _i32(context_lens, "context_lens"), max_context_len,
+        block_tables.shape[1], block_size, layout, _i32(context_lens, "context_lens"),
+        max_context_len,
         dt, scale, split_tokens, wp, wn, _stream(config)))
 
 

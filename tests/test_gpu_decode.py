@@ -152,8 +152,9 @@ def make_paged(rng, lens, Hkv, d, bs, kind):
     return kc, vc, kp, vp, bt
 
 
+@pytest.mark.parametrize("layout", [K.KV_LAYOUT_TOKEN_MAJOR, K.KV_LAYOUT_HEAD_MAJOR])
 @pytest.mark.parametrize("kind", ["fp16", "bf16", "fp32"])
-def test_paged_equals_contiguous_bit_exact(kind):
+def test_paged_equals_contiguous_bit_exact(kind, layout):
     rng = np.random.default_rng(11)
     B, Hq, Hkv, d, bs = 6, 32, 8, 128, 16
     lens = np.array([1, 17, 300, 512, 1000, 2049], np.int32)
@@ -166,8 +167,11 @@ def test_paged_equals_contiguous_bit_exact(kind):
         op = torch.zeros_like(oc)
         K.batched_decode_cu(dev(q, kind), dev(kc, kind), dev(vc, kind), oc, lens_d, maxlen, Hkv,
                             split_tokens=split)
-        K.paged_decode_cu(dev(q, kind), dev(kp, kind), dev(vp, kind), op,
-                          torch.from_numpy(bt).cuda(), lens_d, maxlen, split_tokens=split)
+        kpl, vpl = (kp, vp) if layout == K.KV_LAYOUT_TOKEN_MAJOR else (
+            kp.transpose(0, 2, 1, 3), vp.transpose(0, 2, 1, 3))
+        K.paged_decode_cu(dev(q, kind), dev(kpl, kind), dev(vpl, kind), op,
+                          torch.from_numpy(bt).cuda(), lens_d, maxlen, split_tokens=split,
+                          layout=layout)
         torch.cuda.synchronize()
         assert torch.equal(oc, op), f"split {split}"
         ref = oracle.decode_contig(q, kc, vc, lens)
@@ -213,8 +217,9 @@ def test_zero_length_rows_give_zeros():
     assert_lowp_close(host(o)[1], ref[1])
 
 
+@pytest.mark.parametrize("layout", [K.KV_LAYOUT_TOKEN_MAJOR, K.KV_LAYOUT_HEAD_MAJOR])
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
-def test_c4_paged_decode_full_size(kind):
+def test_c4_paged_decode_full_size(kind, layout):
     """BASELINE config 4 at full size: batch 32, 32 q / 8 kv heads, d 128, KV lengths
     U[512, 4096], block 16, block tables a random permutation of the pool."""
     rng = np.random.default_rng(0xC4)
@@ -223,8 +228,11 @@ def test_c4_paged_decode_full_size(kind):
     _, _, kp, vp, bt = make_paged(rng, lens, Hkv, d, bs, kind)
     q = quantize(normal(rng, (B, Hq, d)), kind)
     o = torch.zeros(B, Hq, d, device="cuda", dtype=TORCH[kind])
-    K.paged_decode_cu(dev(q, kind), dev(kp, kind), dev(vp, kind), o, torch.from_numpy(bt).cuda(),
-                      torch.from_numpy(lens).cuda(), int(lens.max()))
+    kpl, vpl = (kp, vp) if layout == K.KV_LAYOUT_TOKEN_MAJOR else (
+        kp.transpose(0, 2, 1, 3), vp.transpose(0, 2, 1, 3))
+    K.paged_decode_cu(dev(q, kind), dev(kpl, kind), dev(vpl, kind), o,
+                      torch.from_numpy(bt).cuda(), torch.from_numpy(lens).cuda(),
+                      int(lens.max()), layout=layout)
     torch.cuda.synchronize()
     ref = oracle.decode_paged(q, kp, vp, bt, lens, nthreads=8)
     assert_lowp_close(host(o), ref, what="C4 paged decode")
