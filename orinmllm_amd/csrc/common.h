@@ -108,6 +108,14 @@ __device__ __forceinline__ Chunk<T> load_chunk(const T* p) {
   return c;
 }
 
+// Streaming load: the data is read once, so it should not displace reusable lines.
+template <typename T>
+__device__ __forceinline__ Chunk<T> load_chunk_nt(const T* p) {
+  Chunk<T> c;
+  c.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return c;
+}
+
 // ---------------------------------------------------------------- wave reductions
 // DPP controls (CDNA encoding).
 constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]

@@ -265,7 +265,7 @@ decode_split_kernel(DecodeArgs a) {
                           : (min(t0 + s * 8 + grp, s1 - 1) - step_tok) * (int)map.tok_stride +
                                 k_lane;
 #pragma unroll
-      for (int n = 0; n < NV; ++n) dst[s][n] = load_chunk(rowp + lo + n * S::CH_STRIDE);
+      for (int n = 0; n < NV; ++n) dst[s][n] = load_chunk_nt(rowp + lo + n * S::CH_STRIDE);
     }
   };
   // V token j = 8s + r of the tile lies in the block of K step s; the step's row address
@@ -281,7 +281,7 @@ decode_split_kernel(DecodeArgs a) {
         const int off = full ? v_off[r]
                              : (min(t0 + s * 8 + r, s1 - 1) - step_tok) * (int)map.tok_stride +
                                    v_lane;
-        dst[s * 8 + r] = *reinterpret_cast<const VR*>(rowp + off);
+        dst[s * 8 + r] = __builtin_nontemporal_load(reinterpret_cast<const VR*>(rowp + off));
       }
     }
   };
