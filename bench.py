@@ -31,6 +31,11 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, TFLOP/s
 
 
+def _bytes(t):
+    """HBM bytes per launch (read + written) from the calibrated rocprof counters."""
+    return None if not t else t["read_bytes"] + t["write_bytes"]
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -39,6 +44,9 @@ def parse():
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="also run one 512 MiB device copy (the reference traffic for the "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -95,9 +103,9 @@ def make_decode(dtype, gen, pools, layout=1):
                 maxlen=int(lens.max()))
 
 
-def cpu_baseline(pf, dc):
-    """Time the oracle on the host on a bounded sample: 128 evenly spaced prefill query
-    rows (all heads) and 8 of the 32 decode sequences."""
+def cpu_baseline(pf, dc, min_seconds=8.0):
+    """Time the oracle (all host cores, OpenMP over query rows) on the full C3 prefill and
+    the full C4 decode, repeating each until it has run about min_seconds."""
     import numpy as np
     from oracle import oracle
 
@@ -106,14 +114,16 @@ def cpu_baseline(pf, dc):
     q = pf["q"].float().cpu().numpy()
     k = pf["k"].float().cpu().numpy()
     v = pf["v"].float().cpu().numpy()
-    rows = np.linspace(0, S - 1, 128).astype(np.int64)
-    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=rows[:4], nthreads=threads)  # warm
-    t0 = time.perf_counter()
-    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=rows, nthreads=threads)
-    t_pf = time.perf_counter() - t0
-    flops = float(sum(4.0 * d * Hq * (r + 1) for r in rows))
+    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=np.arange(4), nthreads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while reps < 20 and (reps == 0 or time.perf_counter() - t0 < min_seconds):
+        oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, nthreads=threads)
+        reps += 1
+    t_total = time.perf_counter() - t0
+    t_pf = t_total / reps
+    flops = pf["flops"]
 
-    nseq = 8
+    nseq = dc["B"]
     kp = dc["kp"][0].float().cpu().numpy()
     vp = dc["vp"][0].float().cpu().numpy()
     if dc["layout"] == 1:  # the oracle takes token-major pools
@@ -122,21 +132,29 @@ def cpu_baseline(pf, dc):
     qd = dc["q"][:nseq].float().cpu().numpy()
     bt = dc["bt"][:nseq].cpu().numpy()
     lens = dc["lens"][:nseq]
-    t0 = time.perf_counter()
-    oracle.decode_paged(qd, kp, vp, bt, lens, nthreads=threads)
-    t_dc = time.perf_counter() - t0
+    dreps, t0 = 0, time.perf_counter()
+    while dreps < 200 and (dreps == 0 or time.perf_counter() - t0 < min_seconds / 4):
+        oracle.decode_paged(qd, kp, vp, bt, lens, nthreads=threads)
+        dreps += 1
+    t_dc = (time.perf_counter() - t0) / dreps
     kv_bytes = 2 * int(lens.sum()) * Hkv * d * 2
     return {
         "value": flops / t_pf / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": f"causal prefill rows {len(rows)} of {S} (evenly spaced, all {Hq} heads), "
-                  f"fp32 oracle on fp16-valued inputs, OpenMP over rows; {t_pf:.2f} s",
+        "sample": f"the full C3 causal prefill ({S} rows x {Hq} heads), fp32 oracle on "
+                  f"fp16-valued inputs, OpenMP over rows, {reps} runs in {t_total:.1f} s",
         "decode": {"value": kv_bytes / t_dc / 1e9, "unit": "GB/s",
-                   "sample": f"{nseq} of 32 paged-decode sequences; {t_dc:.2f} s"},
+                   "sample": f"the full C4 paged decode ({nseq} sequences), {dreps} runs, "
+                             f"{t_dc * 1e3:.1f} ms each"},
     }
 
 
 def main():
     args = parse()
+    traffic = {}
+    tpath = os.path.join(REPO, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(every box has one MI355X; see DESIGN.md for how the path shards)",
@@ -207,20 +225,26 @@ def main():
             "prefill_ms": round(pf_ms, 4),
             "decode_ms": round(dc_ms, 4),
             "kv_pools_rotated": args.pools,
+            "traffic_source": traffic.get("source"),
         },
         "roofline": {
             "bound": "mfma", "achieved": round(pf_tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(pf_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": _bytes(traffic.get("fwd_causal_c3")),
         },
         "decode": {
             "metric": "paged decode KV-read GB/s", "value": round(dc_gbs, 1), "unit": "GB/s",
             "kv_bytes_per_call": dc["kv_bytes"],
             "roofline": {"bound": "hbm", "achieved": round(dc_gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(dc_gbs / HBM_PEAK_GBS, 4),
-                         "traffic": None},
+                         "traffic": _bytes(traffic.get("decode_paged_c4"))},
         },
     }
+    if args.calibration_copy:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(pf, dc)
     print(json.dumps(out), flush=True)
