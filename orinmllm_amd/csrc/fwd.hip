@@ -143,6 +143,26 @@ struct TileStage {
 
   __device__ __forceinline__ void load(const T* kb, const T* vb, long tok_stride, int t0,
                                        int kv_end, int tid) {
+    // Whole tile inside the sequence and no padded chunks: unconditional loads.
+    if (t0 + BN <= kv_end && S::DC == S::DKC && S::VU_TOTAL % kFwdThreads == 0 &&
+        (BN * S::DKC) % kFwdThreads == 0 && S::DC * 8 == S::DO) {
+#pragma unroll
+      for (int i = 0; i < S::KCH; ++i) {
+        const int c = tid + i * kFwdThreads;
+        const int row = c / S::DKC, ch = c % S::DKC;
+        k[i] = *reinterpret_cast<const u32x4*>(kb + (long)(t0 + row) * tok_stride + ch * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < S::VU; ++i) {
+        const int u = tid + i * kFwdThreads;
+        const int kb4 = u % (BN / 4), db = u / (BN / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          v[i][r] = *reinterpret_cast<const u32x4*>(vb + (long)(t0 + kb4 * 4 + r) * tok_stride +
+                                                    db * 8);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < S::KCH; ++i) {
       const int c = tid + i * kFwdThreads;
@@ -206,7 +226,8 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
   T* sVbuf = sKbuf + 2 * S::K_ELEMS;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lq = lane & 31, hf = lane >> 5;
 
   int head, q_lo, q_n, seg_start, kv_end, pos_off;
@@ -325,21 +346,29 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[j][kt][r] = 0.f;
+      // K fragments of k-step s+1 are read from LDS before the MFMAs of k-step s issue.
+      u32x4 kf[2][2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+        kf[0][kt] = *reinterpret_cast<const u32x4*>(sK + (kt * 32 + lq) * S::SK + 8 * hf);
 #pragma unroll
       for (int s = 0; s < S::KS; ++s) {
+        if (s + 1 < S::KS) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+            kf[(s + 1) & 1][kt] = *reinterpret_cast<const u32x4*>(
+                sK + (kt * 32 + lq) * S::SK + 16 * (s + 1) + 8 * hf);
+        }
         u32x4 qf[kSub];
 #pragma unroll
         for (int j = 0; j < kSub; ++j)
           qf[j] = S::Q_IN_LDS ? *reinterpret_cast<const u32x4*>(sQw + 32 * j * S::SQ + 16 * s)
                               : qreg[S::Q_IN_LDS ? 0 : j][S::Q_IN_LDS ? 0 : s];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const u32x4 af =
-              *reinterpret_cast<const u32x4*>(sK + (kt * 32 + lq) * S::SK + 16 * s + 8 * hf);
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int j = 0; j < kSub; ++j)
-            if (act[j]) sacc[j][kt] = mfma32<T>(af, qf[j], sacc[j][kt]);
-        }
+            if (act[j]) sacc[j][kt] = mfma32<T>(kf[s & 1][kt], qf[j], sacc[j][kt]);
       }
 
       u32x4 pf[kSub][4];
@@ -348,21 +377,23 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
         if (!act[j]) continue;
         // Mask (causal diagonal / segment tail) and the row max.
         const int qpos = wpos0 + 32 * j + lq;
+        // Uniform per wave: only tiles on the diagonal / past the segment end mask.
         const bool need_mask = CAUSAL ? (t0 + BN - 1 > wpos0 + 32 * j) : (t0 + BN > kv_end);
+        if (need_mask) {
+          const int lim = CAUSAL ? qpos : kv_end - 1;  // last key this lane's query sees
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kp = t0 + kt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+              sacc[j][kt][r] = kp > lim ? -INFINITY : sacc[j][kt][r];
+            }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = sacc[j][kt][r];
-            if (need_mask) {
-              const int kp = t0 + kt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-              const bool dead = CAUSAL ? (kp > qpos) : (kp >= kv_end);
-              x = dead ? -INFINITY : x;
-              sacc[j][kt][r] = x;
-            }
-            mx = fmaxf(mx, x);
-          }
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[j][kt][r]);
         mx = pair_max(mx) * c;
         // Lazy rescale: raise the exponent offset only when the max grew by > 2^8.
         const float m_old = m_use[j];
@@ -390,17 +421,23 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
         l_run[j] = ls;
       }
 
-      // O^T += V^T . P^T over the 4 16-key chunks of the tile.
+      // O^T += V^T . P^T over the 4 16-key chunks of the tile; the V fragment of the
+      // next (chunk, d-tile) is read from LDS before the current MFMAs issue.
+      constexpr int NPV = 4 * S::OT;
+      u32x4 vf[2];
+      vf[0] = *reinterpret_cast<const u32x4*>(sV + lq * S::SV + 8 * hf);
 #pragma unroll
-      for (int ck = 0; ck < 4; ++ck)
-#pragma unroll
-        for (int t = 0; t < S::OT; ++t) {
-          const u32x4 af =
-              *reinterpret_cast<const u32x4*>(sV + (t * 32 + lq) * S::SV + 16 * ck + 8 * hf);
-#pragma unroll
-          for (int j = 0; j < kSub; ++j)
-            if (act[j]) oacc[j][t] = mfma32<T>(af, pf[j][ck], oacc[j][t]);
+      for (int n = 0; n < NPV; ++n) {
+        const int ck = n / S::OT, t = n % S::OT;
+        if (n + 1 < NPV) {
+          const int ck1 = (n + 1) / S::OT, t1 = (n + 1) % S::OT;
+          vf[(n + 1) & 1] = *reinterpret_cast<const u32x4*>(sV + (t1 * 32 + lq) * S::SV +
+                                                            16 * ck1 + 8 * hf);
         }
+#pragma unroll
+        for (int j = 0; j < kSub; ++j)
+          if (act[j]) oacc[j][t] = mfma32<T>(vf[n & 1], pf[j][ck], oacc[j][t]);
+      }
     }
 
     if (more) {
