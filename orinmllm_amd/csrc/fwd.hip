@@ -8,15 +8,15 @@
 //    (replaces the cuBLAS QK^T / softmax / PV / transpose sequence of
 //     vision_attention_pretransposed_cu, vision_encoder_kernel.cu:954-1021).
 //
-// Work decomposition.  A workgroup of 4 waves (one per SIMD) owns BM = 256 query rows
-// of one query head; each wave owns 64 rows as two 32-row sub-blocks.  The Q rows sit
-// in LDS for the whole kernel; key/value tiles of BN = 64 rows are staged in LDS
-// (double-buffered, one barrier per tile) and shared by the 4 waves.  Every K or V fragment read from LDS feeds two MFMAs (one per
-// sub-block), which halves LDS traffic per MFMA relative to one sub-block per wave.
+// Work decomposition.  A workgroup of NW = 4 waves owns BM = 32*NW query rows of one
+// query head; each wave owns 32 rows whose Q fragments stay in registers.  Key/value tiles of BN = 64 rows are
+// staged in LDS (double-buffered through registers, one barrier per tile) and shared by
+// the waves.  Two waves share each SIMD, so one wave's softmax VALU work can fill the
+// other's MFMA cycles.
 //
-// Per wave, sub-block and tile, with v_mfma_f32_32x32x16_{f16,bf16}:
-//   S^T[key][q] = K . Q^T      A = K rows from LDS (one 16-byte ds_read per lane),
-//                              B = Q fragment from LDS (one 16-byte ds_read per lane).
+// Per wave and tile, with v_mfma_f32_32x32x16_{f16,bf16}:
+//   S^T[key][q] = K . Q^T      A = K rows from LDS (one 16-byte ds_read per lane, read
+//                              one k-step ahead), B = Q fragment in registers.
 //   The 32x32 accumulator layout puts one query column in each lane (lane l holds
 //   query l%32 and 16 key rows), so the row max / row sum of the online softmax are
 //   in-lane reductions plus one v_permlane32_swap with lane l^32.
@@ -29,9 +29,11 @@
 //
 // Softmax: exp2 with the scale folded into one FMA; the running max used in the
 // exponent is only raised when a row's max grows by more than 2^8 (lazy rescale: the
-// weights stay <= 256, exact in fp16/bf16 range, and O is rescaled only when some lane
+// weights stay <= 256, inside fp16/bf16 range, and O is rescaled only when some lane
 // of the wave needs it); row sums come from v_dot2 on the packed 16-bit weights, so
-// the normaliser is the sum of exactly the weights the PV MFMA used.
+// the normaliser is the sum of exactly the weights the PV MFMA used.  The QK^T MFMAs
+// run at raised wave priority (s_setprio 1), which measured faster than no priority
+// change and than raising it around the PV MFMAs as well.
 //
 // Scheduling: causal blocks start longest-first.  When the kv heads split evenly over
 // the 8 XCDs, block i (dispatched to XCD i % 8) serves a query head of kv head
@@ -43,22 +45,16 @@ namespace orin {
 
 namespace {
 
-constexpr int kFwdWaves = 4;
-constexpr int kFwdThreads = kFwdWaves * kWave;
-constexpr int BN = 64;                  // key rows per tile
+constexpr int BN = 64;                // key rows per tile
 constexpr int kXcds = 8;
-#ifndef FWD_SUB
-#define FWD_SUB 1
-#endif
-constexpr float kLazyRescale = 8.0f;    // log2 growth of the row max that forces a rescale
+constexpr float kLazyRescale = 8.0f;  // log2 growth of the row max that forces a rescale
 
-template <int D, int SUB>
+template <int D, int NW>
 struct FwdShape {
-  // SUB 32-row query sub-blocks per wave; with SUB > 1 every K/V fragment read from LDS
-  // feeds SUB MFMAs, and the Q rows live in LDS to leave registers for the accumulators.
-  static constexpr int BM = 32 * SUB * kFwdWaves;  // query rows per workgroup
-  static constexpr bool Q_IN_LDS = SUB > 1;
   static_assert(D % 8 == 0, "head size must be a multiple of 8");
+  static_assert(NW == 2 || NW == 4, "2 or 4 waves per workgroup");
+  static constexpr int THREADS = NW * kWave;
+  static constexpr int BM = 32 * NW;             // query rows per workgroup
   static constexpr int DK = (D + 15) / 16 * 16;  // contraction length of QK^T
   static constexpr int DO = (D + 31) / 32 * 32;  // output rows of O^T
   static constexpr int KS = DK / 16;             // MFMA k-steps for QK^T
@@ -69,12 +65,13 @@ struct FwdShape {
   static constexpr int SV = BN + 8;              // LDS V^T row stride (elements)
   static constexpr int K_ELEMS = BN * SK;        // one K buffer
   static constexpr int V_ELEMS = DO * SV;        // one V^T buffer
-  static constexpr int KCH = (BN * DKC + kFwdThreads - 1) / kFwdThreads;  // K chunks / thread
-  static constexpr int VU_TOTAL = (BN / 4) * (DO / 8);                    // 4x8 V units
-  static constexpr int VU = (VU_TOTAL + kFwdThreads - 1) / kFwdThreads;   // V units / thread
-  static constexpr int SQ = DK + 8;              // LDS Q row stride (elements)
-  static constexpr int Q_ELEMS = Q_IN_LDS ? BM * SQ : 0;  // the workgroup's Q rows
-  static constexpr size_t LDS_BYTES = (2 * (K_ELEMS + V_ELEMS) + Q_ELEMS) * 2;
+  static constexpr int KCH = (BN * DKC + THREADS - 1) / THREADS;  // K chunks / thread
+  static constexpr int VU_TOTAL = (BN / 4) * (DO / 8);            // 4-key x 8-dim V units
+  static constexpr int VU = (VU_TOTAL + THREADS - 1) / THREADS;   // V units / thread
+  // Every thread's chunks are real data (no padding, no partial last pass).
+  static constexpr bool EXACT = DC == DKC && DC * 8 == DO && VU_TOTAL % THREADS == 0 &&
+                                (BN * DKC) % THREADS == 0;
+  static constexpr size_t LDS_BYTES = 2 * (K_ELEMS + V_ELEMS) * 2;  // double-buffered
 };
 
 template <typename T>
@@ -135,26 +132,24 @@ __device__ __forceinline__ int vt_pos(int k) {
 }
 
 // Register staging of one K/V tile: global -> registers, then registers -> LDS.
-template <typename T, int D>
+template <typename T, int D, int NW>
 struct TileStage {
-  using S = FwdShape<D, 1>;
+  using S = FwdShape<D, NW>;
   u32x4 k[S::KCH];
   u32x4 v[S::VU][4];
 
   __device__ __forceinline__ void load(const T* kb, const T* vb, long tok_stride, int t0,
                                        int kv_end, int tid) {
-    // Whole tile inside the sequence and no padded chunks: unconditional loads.
-    if (t0 + BN <= kv_end && S::DC == S::DKC && S::VU_TOTAL % kFwdThreads == 0 &&
-        (BN * S::DKC) % kFwdThreads == 0 && S::DC * 8 == S::DO) {
+    if (S::EXACT && t0 + BN <= kv_end) {  // whole tile inside the sequence: no guards
 #pragma unroll
       for (int i = 0; i < S::KCH; ++i) {
-        const int c = tid + i * kFwdThreads;
+        const int c = tid + i * S::THREADS;
         const int row = c / S::DKC, ch = c % S::DKC;
         k[i] = *reinterpret_cast<const u32x4*>(kb + (long)(t0 + row) * tok_stride + ch * 8);
       }
 #pragma unroll
       for (int i = 0; i < S::VU; ++i) {
-        const int u = tid + i * kFwdThreads;
+        const int u = tid + i * S::THREADS;
         const int kb4 = u % (BN / 4), db = u / (BN / 4);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -165,7 +160,7 @@ struct TileStage {
     }
 #pragma unroll
     for (int i = 0; i < S::KCH; ++i) {
-      const int c = tid + i * kFwdThreads;
+      const int c = tid + i * S::THREADS;
       const int row = c / S::DKC, ch = c % S::DKC;
       u32x4 val = {0u, 0u, 0u, 0u};
       if (c < BN * S::DKC && ch < S::DC && t0 + row < kv_end)
@@ -174,7 +169,7 @@ struct TileStage {
     }
 #pragma unroll
     for (int i = 0; i < S::VU; ++i) {
-      const int u = tid + i * kFwdThreads;
+      const int u = tid + i * S::THREADS;
       const int kb4 = u % (BN / 4), db = u / (BN / 4);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -190,7 +185,7 @@ struct TileStage {
   __device__ __forceinline__ void store(T* sK, T* sV, int tid) const {
 #pragma unroll
     for (int i = 0; i < S::KCH; ++i) {
-      const int c = tid + i * kFwdThreads;
+      const int c = tid + i * S::THREADS;
       if (c < BN * S::DKC) {
         const int row = c / S::DKC, ch = c % S::DKC;
         *reinterpret_cast<u32x4*>(sK + row * S::SK + ch * 8) = k[i];
@@ -198,17 +193,18 @@ struct TileStage {
     }
 #pragma unroll
     for (int i = 0; i < S::VU; ++i) {
-      const int u = tid + i * kFwdThreads;
+      const int u = tid + i * S::THREADS;
       if (u < S::VU_TOTAL) {
         const int kb4 = u % (BN / 4), db = u / (BN / 4);
         const int pos = vt_pos(kb4 * 4);
         // 4 keys x 8 dims -> 8 rows (dims) of 4 consecutive keys.
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int w = e >> 1, sh = (e & 1) * 16;
-          const uint32_t x0 = (v[i][0][w] >> sh) & 0xffffu, x1 = (v[i][1][w] >> sh) & 0xffffu;
-          const uint32_t x2 = (v[i][2][w] >> sh) & 0xffffu, x3 = (v[i][3][w] >> sh) & 0xffffu;
-          u32x2 pk = {x0 | (x1 << 16), x2 | (x3 << 16)};
+          // element e of keys (0,1) and (2,3): one v_perm_b32 per packed pair
+          const int w = e >> 1;
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          u32x2 pk = {__builtin_amdgcn_perm(v[i][1][w], v[i][0][w], sel),
+                      __builtin_amdgcn_perm(v[i][3][w], v[i][2][w], sel)};
           *reinterpret_cast<u32x2*>(sV + (db * 8 + e) * S::SV + pos) = pk;
         }
       }
@@ -216,10 +212,9 @@ struct TileStage {
   }
 };
 
-template <typename T, int D, int SUB, bool CAUSAL>
-__global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdArgs a) {
-  using S = FwdShape<D, SUB>;
-  constexpr int kSub = SUB;
+template <typename T, int D, int NW, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) fwd_kernel(FwdArgs a) {
+  using S = FwdShape<D, NW>;
   constexpr int BM = S::BM;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   T* sKbuf = reinterpret_cast<T*>(smem);
@@ -268,59 +263,38 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
   const T* vb = reinterpret_cast<const T*>(a.v) + (long)seg_start * a.kv_tok_stride +
                 (long)kvh * a.kv_head_stride;
 
-  // Q fragments: sub-block j, query row q_lo + wave*32*SUB + 32j + lq, dims
-  // 16s + 8hf + 0..7.  With SUB > 1 the workgroup's Q rows go to LDS once (zero-padded
-  // to DK and past q_n) and each wave reads its fragments per k-step, which keeps
-  // registers free for the accumulators; with SUB == 1 they stay in registers.
-  const int wq0 = q_lo + wave * 32 * kSub;  // first local query of the wave
-  T* sQ = sVbuf + 2 * S::V_ELEMS;
-  u32x4 qreg[S::Q_IN_LDS ? 1 : kSub][S::Q_IN_LDS ? 1 : S::KS];
-  if constexpr (S::Q_IN_LDS) {
-    for (int c = tid; c < BM * S::DKC; c += kFwdThreads) {
-      const int row = c / S::DKC, ch = c % S::DKC;
-      const int qi = q_lo + row;
+  // Q fragment of this lane: query row wq0 + lq, dims 16s + 8hf + 0..7 of k-step s.
+  const int wq0 = q_lo + wave * 32;  // first local query of the wave
+  const int qi = wq0 + lq;
+  u32x4 qf[S::KS];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q) + (long)(seg_start + qi) * a.q_tok_stride +
+                  (long)head * a.q_head_stride;
+#pragma unroll
+    for (int s = 0; s < S::KS; ++s) {
+      const int d0 = 16 * s + 8 * hf;
       u32x4 val = {0u, 0u, 0u, 0u};
-      if (qi < q_n && ch < S::DC)
-        val = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.q) +
-                                              (long)(seg_start + qi) * a.q_tok_stride +
-                                              (long)head * a.q_head_stride + ch * 8);
-      *reinterpret_cast<u32x4*>(sQ + row * S::SQ + ch * 8) = val;
+      if (qi < q_n && d0 < D) val = *reinterpret_cast<const u32x4*>(qp + d0);
+      qf[s] = val;
     }
-  } else {
+    // Settle the Q loads here: without this the loop-header wait merges them with the
+    // next tile's prefetch and waits for all outstanding loads (vmcnt(0)) every tile.
 #pragma unroll
-    for (int j = 0; j < kSub; ++j) {
-      const int qi = wq0 + 32 * j + lq;
-      const T* qp = reinterpret_cast<const T*>(a.q) + (long)(seg_start + qi) * a.q_tok_stride +
-                    (long)head * a.q_head_stride;
-#pragma unroll
-      for (int s = 0; s < S::KS; ++s) {
-        const int d0 = 16 * s + 8 * hf;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (qi < q_n && d0 < D) val = *reinterpret_cast<const u32x4*>(qp + d0);
-        qreg[S::Q_IN_LDS ? 0 : j][S::Q_IN_LDS ? 0 : s] = val;
-      }
-    }
+    for (int s = 0; s < S::KS; ++s) __asm__ volatile("" : "+v"(qf[s]));
   }
-  const T* sQw = sQ + (wave * 32 * kSub + lq) * S::SQ + 8 * hf;
 
-  f32x16 oacc[kSub][S::OT];
+  f32x16 oacc[S::OT];
 #pragma unroll
-  for (int j = 0; j < kSub; ++j)
+  for (int t = 0; t < S::OT; ++t)
 #pragma unroll
-    for (int t = 0; t < S::OT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[j][t][r] = 0.f;
-  float m_use[kSub], l_run[kSub];
-#pragma unroll
-  for (int j = 0; j < kSub; ++j) {
-    m_use[j] = -INFINITY;
-    l_run[j] = 0.f;
-  }
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+  float m_use = -INFINITY, l_run = 0.f;
   const float c = a.scale_log2;
   const int wpos0 = pos_off + wq0;  // position of the wave's first query
+  const int qpos = wpos0 + lq;      // position of this lane's query
 
   const int n_tiles = (kv_end + BN - 1) / BN;
-  TileStage<T, D> stage;
+  TileStage<T, D, NW> stage;
   stage.load(kb, vb, a.kv_tok_stride, 0, kv_end, tid);
   stage.store(sKbuf, sVbuf, tid);
   __syncthreads();
@@ -332,21 +306,16 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
     const bool more = it + 1 < n_tiles;
     if (more) stage.load(kb, vb, a.kv_tok_stride, t0 + BN, kv_end, tid);
 
-    // Sub-block j is active if some of its queries see key t0 (causal).
-    bool act[kSub];
+    // Causal: tiles wholly above this wave's diagonal contribute nothing.
+    if (!CAUSAL || t0 <= wpos0 + 31) {
+      // S^T = K . Q^T for keys t0..t0+63 (two 32-key halves); the K fragments of
+      // k-step s+1 are read from LDS before the MFMAs of k-step s issue.
+      f32x16 sacc[2];
 #pragma unroll
-    for (int j = 0; j < kSub; ++j) act[j] = !CAUSAL || t0 <= wpos0 + 32 * j + 31;
-
-    if (act[kSub - 1]) {
-      // S^T = K . Q^T for keys t0..t0+63 (two 32-key halves), both sub-blocks.
-      f32x16 sacc[kSub][2];
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int j = 0; j < kSub; ++j)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[j][kt][r] = 0.f;
-      // K fragments of k-step s+1 are read from LDS before the MFMAs of k-step s issue.
+        for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+      __builtin_amdgcn_s_setprio(1);
       u32x4 kf[2][2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -359,70 +328,57 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
             kf[(s + 1) & 1][kt] = *reinterpret_cast<const u32x4*>(
                 sK + (kt * 32 + lq) * S::SK + 16 * (s + 1) + 8 * hf);
         }
-        u32x4 qf[kSub];
 #pragma unroll
-        for (int j = 0; j < kSub; ++j)
-          qf[j] = S::Q_IN_LDS ? *reinterpret_cast<const u32x4*>(sQw + 32 * j * S::SQ + 16 * s)
-                              : qreg[S::Q_IN_LDS ? 0 : j][S::Q_IN_LDS ? 0 : s];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int j = 0; j < kSub; ++j)
-            if (act[j]) sacc[j][kt] = mfma32<T>(kf[s & 1][kt], qf[j], sacc[j][kt]);
+        for (int kt = 0; kt < 2; ++kt) sacc[kt] = mfma32<T>(kf[s & 1][kt], qf[s], sacc[kt]);
       }
+      __builtin_amdgcn_s_setprio(0);
 
-      u32x4 pf[kSub][4];
-#pragma unroll
-      for (int j = 0; j < kSub; ++j) {
-        if (!act[j]) continue;
-        // Mask (causal diagonal / segment tail) and the row max.
-        const int qpos = wpos0 + 32 * j + lq;
-        // Uniform per wave: only tiles on the diagonal / past the segment end mask.
-        const bool need_mask = CAUSAL ? (t0 + BN - 1 > wpos0 + 32 * j) : (t0 + BN > kv_end);
-        if (need_mask) {
-          const int lim = CAUSAL ? qpos : kv_end - 1;  // last key this lane's query sees
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int kp = t0 + kt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-              sacc[j][kt][r] = kp > lim ? -INFINITY : sacc[j][kt][r];
-            }
-        }
-        float mx = -INFINITY;
+      // Mask (wave-uniform test: only tiles on the diagonal / past the segment end).
+      const bool need_mask = CAUSAL ? (t0 + BN - 1 > wpos0) : (t0 + BN > kv_end);
+      if (need_mask) {
+        const int lim = CAUSAL ? qpos : kv_end - 1;  // last key this lane's query sees
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[j][kt][r]);
-        mx = pair_max(mx) * c;
-        // Lazy rescale: raise the exponent offset only when the max grew by > 2^8.
-        const float m_old = m_use[j];
-        const float m_new = (mx > m_old + kLazyRescale) ? mx : m_old;
-        m_use[j] = m_new;
-        if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {
-          const float alpha = fast_exp2(m_old - m_new);  // 1 where unchanged
-          l_run[j] *= alpha;
-#pragma unroll
-          for (int t = 0; t < S::OT; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[j][t][r] *= alpha;
-        }
-        float ls = l_run[j];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; r += 2) {
-            const float p0 = fast_exp2(__builtin_fmaf(sacc[j][kt][r], c, -m_new));
-            const float p1 = fast_exp2(__builtin_fmaf(sacc[j][kt][r + 1], c, -m_new));
-            const uint32_t pk = pack2<T>(p0, p1);
-            pf[j][kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
-            ls = sum_pair<T>(pk, ls);
+          for (int r = 0; r < 16; ++r) {
+            const int kp = t0 + kt * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+            sacc[kt][r] = kp > lim ? -INFINITY : sacc[kt][r];
           }
-        l_run[j] = ls;
       }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+      mx = pair_max(mx) * c;
+      // Lazy rescale: raise the exponent offset only when the max grew by > 2^8.
+      const float m_old = m_use;
+      const float m_new = (mx > m_old + kLazyRescale) ? mx : m_old;
+      m_use = m_new;
+      if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {
+        const float alpha = fast_exp2(m_old - m_new);  // 1 where unchanged
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < S::OT; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+      }
+      u32x4 pf[4];
+      float ls = l_run;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -m_new));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[kt][r + 1], c, -m_new));
+          const uint32_t pk = pack2<T>(p0, p1);
+          pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
+          ls = sum_pair<T>(pk, ls);
+        }
+      l_run = ls;
 
       // O^T += V^T . P^T over the 4 16-key chunks of the tile; the V fragment of the
-      // next (chunk, d-tile) is read from LDS before the current MFMAs issue.
+      // next (chunk, d-tile) is read from LDS before the current MFMA issues.
       constexpr int NPV = 4 * S::OT;
       u32x4 vf[2];
       vf[0] = *reinterpret_cast<const u32x4*>(sV + lq * S::SV + 8 * hf);
@@ -434,9 +390,7 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
           vf[(n + 1) & 1] = *reinterpret_cast<const u32x4*>(sV + (t1 * 32 + lq) * S::SV +
                                                             16 * ck1 + 8 * hf);
         }
-#pragma unroll
-        for (int j = 0; j < kSub; ++j)
-          if (act[j]) oacc[j][t] = mfma32<T>(vf[n & 1], pf[j][ck], oacc[j][t]);
+        oacc[t] = mfma32<T>(vf[n & 1], pf[ck], oacc[t]);
       }
     }
 
@@ -446,63 +400,68 @@ __global__ void __launch_bounds__(kFwdThreads, SUB == 1 ? 2 : 1) fwd_kernel(FwdA
     }
   }
 
-  // Normalise and store: lane holds dims t*32 + 8*(r/4) + 4*hf + r%4 of its query.
+  // Normalise and store: the lane holds dims t*32 + 8*(r/4) + 4*hf + r%4 of its query.
+  const float inv = 1.f / pair_sum(l_run);
+  if (qi < q_n) {
+    T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
+            (long)head * a.o_head_stride;
 #pragma unroll
-  for (int j = 0; j < kSub; ++j) {
-    const int qi = wq0 + 32 * j + lq;
-    const float inv = 1.f / pair_sum(l_run[j]);
-    if (qi < q_n) {
-      T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
-              (long)head * a.o_head_stride;
+    for (int t = 0; t < S::OT; ++t)
 #pragma unroll
-      for (int t = 0; t < S::OT; ++t)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int d0 = t * 32 + 8 * rg + 4 * hf;
-          if (d0 < D) {
-            u32x2 pk = {pack2<T>(oacc[j][t][4 * rg] * inv, oacc[j][t][4 * rg + 1] * inv),
-                        pack2<T>(oacc[j][t][4 * rg + 2] * inv, oacc[j][t][4 * rg + 3] * inv)};
-            *reinterpret_cast<u32x2*>(op + d0) = pk;
-          }
+      for (int rg = 0; rg < 4; ++rg) {
+        const int d0 = t * 32 + 8 * rg + 4 * hf;
+        if (d0 < D) {
+          u32x2 pk = {pack2<T>(oacc[t][4 * rg] * inv, oacc[t][4 * rg + 1] * inv),
+                      pack2<T>(oacc[t][4 * rg + 2] * inv, oacc[t][4 * rg + 3] * inv)};
+          *reinterpret_cast<u32x2*>(op + d0) = pk;
         }
-    }
+      }
   }
 }
 
-template <typename T, int D, int SUB, bool CAUSAL>
+template <int BM, bool CAUSAL>
+long fwd_blocks(const FwdArgs& a) {
+  if (CAUSAL) return (long)((a.n_q + BM - 1) / BM) * a.Hq;
+  return (long)a.n_seg * ((a.max_seqlen + BM - 1) / BM) * a.Hq;
+}
+
+template <typename T, int D, int NW, bool CAUSAL>
 hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t stream) {
-  constexpr int BM = FwdShape<D, SUB>::BM;
-  long blocks;
-  if (CAUSAL)
-    blocks = (long)((a.n_q + BM - 1) / BM) * a.Hq;
-  else
-    blocks = (long)a.n_seg * ((a.max_seqlen + BM - 1) / BM) * a.Hq;
+  using S = FwdShape<D, NW>;
+  const long blocks = fwd_blocks<S::BM, CAUSAL>(a);
   if (blocks <= 0) return hipSuccess;
-  constexpr size_t lds = FwdShape<D, SUB>::LDS_BYTES;
   // The dynamic-LDS limit is a per-device function attribute: set it once per device.
   static unsigned long long configured = 0;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev >= 64 || !(__atomic_load_n(&configured, __ATOMIC_ACQUIRE) & (1ull << dev))) {
-    e = hipFuncSetAttribute((const void*)fwd_kernel<T, D, SUB, CAUSAL>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    e = hipFuncSetAttribute((const void*)fwd_kernel<T, D, NW, CAUSAL>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS_BYTES);
     if (e != hipSuccess) return e;
     if (dev < 64) __atomic_fetch_or(&configured, 1ull << dev, __ATOMIC_RELEASE);
   }
-  hipLaunchKernelGGL((fwd_kernel<T, D, SUB, CAUSAL>), dim3((unsigned)blocks), dim3(kFwdThreads),
-                     lds, stream, a);
+  hipLaunchKernelGGL((fwd_kernel<T, D, NW, CAUSAL>), dim3((unsigned)blocks), dim3(S::THREADS),
+                     S::LDS_BYTES, stream, a);
   return hipGetLastError();
+}
+
+// 4-wave workgroups.  A 2-wave variant (BM = 64) for grids below two workgroups per CU
+// measured no faster on Qwen3-VL-2B-sized prefill (12 heads, 2048 tokens): there the
+// longest causal block, not the grid size, bounds the time.
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_fwd_w(const FwdArgs& a, hipStream_t stream) {
+  return launch_fwd_t<T, D, 4, CAUSAL>(a, stream);
 }
 
 template <bool CAUSAL, typename T>
 hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   switch (a.head_size) {
-    case 64: return launch_fwd_t<T, 64, FWD_SUB, CAUSAL>(a, stream);
-    case 72: return launch_fwd_t<T, 72, FWD_SUB, CAUSAL>(a, stream);
-    case 80: return launch_fwd_t<T, 80, FWD_SUB, CAUSAL>(a, stream);
-    case 96: return launch_fwd_t<T, 96, FWD_SUB, CAUSAL>(a, stream);
-    case 128: return launch_fwd_t<T, 128, FWD_SUB, CAUSAL>(a, stream);
+    case 64: return launch_fwd_w<T, 64, CAUSAL>(a, stream);
+    case 72: return launch_fwd_w<T, 72, CAUSAL>(a, stream);
+    case 80: return launch_fwd_w<T, 80, CAUSAL>(a, stream);
+    case 96: return launch_fwd_w<T, 96, CAUSAL>(a, stream);
+    case 128: return launch_fwd_w<T, 128, CAUSAL>(a, stream);
   }
   return hipErrorInvalidValue;
 }
