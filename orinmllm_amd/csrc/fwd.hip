@@ -41,6 +41,8 @@
 #include "common.h"
 #include "kernels.h"
 
+#include <stdlib.h>
+
 namespace orin {
 
 namespace {
@@ -466,8 +468,24 @@ hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
+// The ping-pong kernel (256-query workgroups, one per CU) takes head size 128 when its
+// grid covers every CU at least once.
+template <bool CAUSAL>
+bool use_pp(const FwdArgs& a, int dtype) {
+  static const int mode = [] {
+    const char* e = getenv("ORIN_FWD_PP");
+    return e ? atoi(e) : -1;
+  }();
+  if (mode == 0 || !fwd_pp_supports(a, dtype)) return false;
+  if (mode == 1) return true;
+  const long blocks = CAUSAL ? (long)((a.n_q + 255) / 256) * a.Hq
+                             : (long)a.n_seg * ((a.max_seqlen + 255) / 256) * a.Hq;
+  return blocks >= 256;
+}
+
 template <bool CAUSAL>
 hipError_t launch_fwd(const FwdArgs& a, int dtype, hipStream_t stream) {
+  if (use_pp<CAUSAL>(a, dtype)) return launch_fwd_pp(a, dtype, CAUSAL, stream);
   if (dtype == kF16) return launch_fwd_d<CAUSAL, f16>(a, stream);
   if (dtype == kBF16) return launch_fwd_d<CAUSAL, bf16>(a, stream);
   return hipErrorInvalidValue;

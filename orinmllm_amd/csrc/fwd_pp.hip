@@ -1,0 +1,523 @@
+// Ping-pong attention forward for head size 128 on gfx950 (fp16 / bf16 in, fp32 accumulate).
+//
+// Serves the same two paths as fwd.hip (causal GQA prefill over a kuiper KV cache,
+// flash_attention_kernel.cu:554-905; bidirectional varlen attention,
+// vision_encoder_kernel.cu:954-1021) when the grid is large enough to fill the chip
+// with 256-query workgroups.
+//
+// Work decomposition.  A workgroup of 8 waves owns 256 query rows of one query head;
+// each wave owns 32 rows (Q fragments in registers).  The waves form two groups of four,
+// one wave of each group per SIMD.  Time is cut into steps separated by workgroup
+// barriers; in every step one group runs its MFMA phase while the other runs its softmax
+// phase, so the SIMD's matrix pipe and its VALU work for different waves at the same
+// time:
+//   MFMA phase M(t):  S(t+1)^T = K(t+1) . Q^T     (16 v_mfma_f32_32x32x16)
+//                     O^T     += V(t)^T . P(t)^T  (16 v_mfma_f32_32x32x16)
+//   softmax phase V(t): mask, row max, lazy rescale, exp2, P(t+1) packed to 16 bits.
+// Group 0 runs M at even steps, group 1 at odd steps.
+//
+// K/V tiles (64 keys) reach LDS through global_load_lds_dwordx4 (no register staging),
+// in a ring of three stages; stage u holds K(u) and V(u-1) and is read in steps 2u and
+// 2u+1.  Every wave moves 1/8 of a stage (four 1 KB transfers) and waits for its own
+// transfers with vmcnt before the barrier that publishes them.
+//   K rows are stored row-major with 16-byte chunk c of row r at chunk c ^ (r & 15):
+//   the K fragment reads (one row per lane, same chunk) are then conflict-free.
+//   V rows are stored row-major with chunk c of row r at chunk c ^ 4(r & 3) and read
+//   with ds_read_b64_tr_b16, which transposes 16-bit elements across 16 lanes: each
+//   read hands a lane four consecutive keys of one dimension, so V^T fragments come
+//   straight from the row-major tile.
+#include "common.h"
+#include "kernels.h"
+
+#include <type_traits>
+
+namespace orin {
+
+namespace {
+
+constexpr int PD = 128;            // head size
+constexpr int PBN = 64;            // keys per tile
+constexpr int PNW = 8;             // waves per workgroup
+constexpr int PBM = 32 * PNW;      // query rows per workgroup
+constexpr int PTHREADS = PNW * kWave;
+constexpr int PSTAGES = 3;         // LDS ring depth
+constexpr int PTILE_BYTES = PBN * PD * 2;              // 16 KB
+constexpr int PKREGION = PSTAGES * PTILE_BYTES;        // K ring, then V ring
+constexpr int PLDS_BYTES = 2 * PKREGION;               // 96 KB
+constexpr int kXcdsPP = 8;
+constexpr float kLazyRescalePP = 8.0f;
+#ifndef PP_PF
+#define PP_PF 3
+#endif
+constexpr int PF = PP_PF;  // LDS reads run this many MFMAs ahead of their use
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) const char* lds_ptr;
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<f16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<bf16>(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, T2{(T)x, (T)y});
+}
+
+template <typename T>
+__device__ __forceinline__ float sum_pair(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float sum_pair<f16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), f16x2{(f16)1.0f, (f16)1.0f}, acc,
+                                false);
+}
+template <>
+__device__ __forceinline__ float sum_pair<bf16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
+                                         bf16x2{(bf16)1.0f, (bf16)1.0f}, acc, false);
+}
+
+// x of lane l^32 (see fwd.hip: the second operand must be an opaque copy).
+__device__ __forceinline__ float partner32(float x) {
+  int y;
+  __asm__("v_mov_b32 %0, %1" : "=v"(y) : "v"(__builtin_bit_cast(int, x)));
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), y, false, false);
+  return __builtin_bit_cast(float, (__lane_id() < 32) ? r[1] : r[0]);
+}
+
+// s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that the scheduler may not move any instruction across.
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane l's data
+// lands at LDS byte lds_addr + 16 l.  Issued from inline asm so that the compiler does
+// not treat it as an LDS store to wait for before every later LDS read: the kernel
+// orders these transfers itself (vmcnt wait + barrier before the stage is read).
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+  __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                   :
+                   : "v"(gptr), "s"(lds_addr)
+                   : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// LDS reads at a per-lane address plus a compile-time offset (folded into the
+// instruction's offset field).
+__device__ __forceinline__ u32x4 lds_read128(lds_ptr p, int byte_off) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(p + byte_off);
+}
+
+__device__ __forceinline__ u32x2 lds_read_tr(lds_ptr p, int byte_off) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + byte_off));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <typename T, bool CAUSAL>
+__global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#ifndef PP_GRP
+#define PP_GRP 0
+#endif
+  const int grp = PP_GRP == 0 ? (wave >> 2) : (wave & 1);
+  const int lq = lane & 31, hf = lane >> 5;
+
+  // ------------------------------------------------------------ block -> (head, rows)
+  int head, q_lo, q_n, seg_start, kv_end, pos_off;
+  if (CAUSAL) {
+    const int nqb = (a.n_q + PBM - 1) / PBM;
+    int qb;
+    if (a.Hkv % kXcdsPP == 0) {
+      const int x = (int)blockIdx.x % kXcdsPP, i = (int)blockIdx.x / kXcdsPP;
+      const int hpx = a.Hq / kXcdsPP;
+      qb = nqb - 1 - i / hpx;
+      const int hl = i % hpx;
+      head = (x + kXcdsPP * (hl / a.kv_mul)) * a.kv_mul + hl % a.kv_mul;
+    } else {
+      qb = nqb - 1 - (int)blockIdx.x / a.Hq;
+      head = (int)blockIdx.x % a.Hq;
+    }
+    q_lo = qb * PBM;
+    q_n = a.n_q;
+    seg_start = 0;
+    pos_off = a.start_pos;
+    kv_end = a.start_pos + min(q_lo + PBM, a.n_q);
+  } else {
+    const int nqb = (a.max_seqlen + PBM - 1) / PBM;
+    head = (int)blockIdx.x % a.Hq;
+    const int rest = (int)blockIdx.x / a.Hq;
+    const int qb = rest % nqb, seg = rest / nqb;
+    seg_start = a.cu_seqlens ? a.cu_seqlens[seg] : 0;
+    q_n = a.cu_seqlens ? a.cu_seqlens[seg + 1] - seg_start : a.n_q;
+    q_lo = qb * PBM;
+    if (q_lo >= q_n) return;
+    pos_off = 0;
+    kv_end = q_n;
+  }
+  const int kvh = head / a.kv_mul;
+  const long tok = a.kv_tok_stride;
+  const T* kb = reinterpret_cast<const T*>(a.k) + (long)seg_start * tok + (long)kvh * a.kv_head_stride;
+  const T* vb = reinterpret_cast<const T*>(a.v) + (long)seg_start * tok + (long)kvh * a.kv_head_stride;
+  const int n_tiles = (kv_end + PBN - 1) / PBN;
+
+  // Row slots interleave the groups (group 0: slots 0,2,4,6; group 1: 1,3,5,7) so both
+  // groups reach the causal diagonal in the same tiles.
+  const int slot = PP_GRP == 0 ? 2 * (wave & 3) + grp : wave;
+  const int wq0 = q_lo + 32 * slot;
+  const int qi = wq0 + lq;
+  const int wpos0 = pos_off + wq0;
+  const int qpos = wpos0 + lq;
+
+  // ------------------------------------------------------------ K/V transfer setup
+  // Transfer i (0,1) of this wave covers rows 4b..4b+3 of a tile, b = 2*wave + i; lane l
+  // moves 16-byte chunk (l%16) of row 4b + l/16 (physical position) whose logical chunk
+  // follows the swizzle of each tile.
+  int k_row[2], k_col[2], v_col[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 4 * (2 * wave + i) + (lane >> 4);
+    const int pc = lane & 15;
+    k_row[i] = row;
+    k_col[i] = 8 * (pc ^ (row & 15));
+    v_col[i] = 8 * (pc ^ (4 * (row & 3)));
+  }
+  char* const k_lds = smem;
+  char* const v_lds = smem + PKREGION;
+  const uint32_t k_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+
+  // Stage u = K(u) + V(u-1) into ring slot u % 3.  Rows past the sequence (and V(-1))
+  // read a valid row instead, so every stage is exactly four transfers per wave and
+  // LDS never holds non-finite garbage.
+  auto issue_stage = [&](int u) __attribute__((always_inline)) {
+    const int sl = u % PSTAGES;
+    const int tk = u * PBN, tv = (u - 1) * PBN;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int b = 2 * wave + i;
+      int rk = tk + k_row[i];
+      rk = rk < kv_end ? rk : kv_end - 1;
+      int rv = tv + k_row[i];
+      rv = rv < 0 ? k_row[i] : (rv < kv_end ? rv : kv_end - 1);
+      dma16(kb + (long)rk * tok + k_col[i], k_base + sl * PTILE_BYTES + b * 1024);
+      dma16(vb + (long)rv * tok + v_col[i], k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
+    }
+  };
+
+  // ------------------------------------------------------------ fragment addresses
+  // K fragment (kt, s): row kt*32 + lq, logical chunk 2s + hf.
+  const lds_ptr lds0 = (lds_ptr)smem;
+  lds_ptr k_p[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) k_p[s] = lds0 + lq * 256 + (((2 * s + hf) ^ (lane & 15)) * 16);
+  // V^T fragment (chunk c of 16 keys, d-tile dt): two transposing reads.  Lane
+  // L = 16g + 4e + q supplies row 16c + 4(g/2) + e (+8 for the second read) and
+  // columns dt*32 + 16(g&1) + 4q .. +3.
+  lds_ptr v_p[4];
+  {
+    const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+    const int row = 4 * (g >> 1) + e;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      v_p[dt] = lds0 + PKREGION + row * 256 + (((dt ^ e) * 4 + 2 * (g & 1) + (q >> 1)) * 16) +
+                (q & 1) * 8;
+  }
+
+  // ------------------------------------------------------------ Q fragments
+  u32x4 qf[8];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q) + (long)(seg_start + qi) * a.q_tok_stride +
+                  (long)head * a.q_head_stride;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (qi < q_n) val = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * hf);
+      qf[s] = val;
+    }
+  }
+
+  // Stages 0..2 up front; wait for stage 0 (younger stages may stay in flight).
+  issue_stage(0);
+  if (n_tiles >= 1) issue_stage(1);
+  if (n_tiles >= 2) issue_stage(2);
+  if (n_tiles >= 2) wait_vmcnt<8>();
+  else wait_vmcnt<4>();
+  step_barrier();
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+  f32x16 sacc[2];
+  u32x4 pf[4];
+  float m_use = -INFINITY, l_run = 0.f;
+  const float c = a.scale_log2;
+
+  auto active = [&](int t) __attribute__((always_inline)) { return !CAUSAL || t * PBN <= wpos0 + 31; };
+
+  // A operands of the MFMA phase.  K fragment (kt, s) of S^T = K . Q^T; V^T fragment
+  // (chunk ck, d-tile dt) of O^T += V^T . P^T, from two transposing reads.
+  // `sl_off` is the ring slot's byte offset (a compile-time constant at every call).
+  auto k_frag = [&](int sl_off, int kt, int s) __attribute__((always_inline)) {
+    return lds_read128(k_p[s], sl_off + kt * 8192);
+  };
+  auto v_frag = [&](int sl_off, int ck, int dt) __attribute__((always_inline)) {
+    const u32x2 lo = lds_read_tr(v_p[dt], sl_off + ck * 16 * 256);
+    const u32x2 hi = lds_read_tr(v_p[dt], sl_off + ck * 16 * 256 + 8 * 256);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
+  // S(0)^T = K(0) . Q^T (K(0) is in ring slot 0).
+  auto qk0 = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+    u32x4 fr[PF + 1];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fr[i] = k_frag(0, i & 1, i >> 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + PF < 16) fr[(i + PF) % (PF + 1)] = k_frag(0, (i + PF) & 1, (i + PF) >> 1);
+      sacc[i & 1] = mfma32<T>(fr[i % (PF + 1)], qf[i >> 1], sacc[i & 1]);
+    }
+  };
+
+  // MFMA phase M(t): S(t+1)^T = K(t+1) . Q^T (when QK) and O^T += V(t)^T . P(t)^T, both
+  // from ring slot (t+1) % 3.  The two products are interleaved (QK, PV, QK, ...) so that
+  // consecutive MFMAs on one accumulator are at least two apart, and every A operand is
+  // read from LDS three MFMAs before its use.
+  auto mphase = [&](auto slot_tag, auto qk_tag) __attribute__((always_inline)) {
+    constexpr bool QK = decltype(qk_tag)::value;
+    constexpr int N = QK ? 32 : 16;
+    constexpr int sl_off = decltype(slot_tag)::value * PTILE_BYTES;
+    if (QK) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+    }
+    // MFMA i: QK step i/2 (even i) or PV step i/2 (odd i) when QK; PV step i otherwise.
+    auto fetch = [&](int i) __attribute__((always_inline)) {
+      if (QK && !(i & 1)) return k_frag(sl_off, (i >> 1) & 1, i >> 2);
+      const int n = QK ? (i >> 1) : i;
+      return v_frag(sl_off, n >> 2, n & 3);
+    };
+    u32x4 fr[PF + 1];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fr[i] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (i + PF < N) fr[(i + PF) % (PF + 1)] = fetch(i + PF);
+      if (QK && !(i & 1)) {
+        const int j = i >> 1;  // QK step: kt = j & 1, s = j >> 1
+        sacc[j & 1] = mfma32<T>(fr[i % (PF + 1)], qf[j >> 1], sacc[j & 1]);
+      } else {
+        const int n = QK ? (i >> 1) : i;
+        oacc[n & 3] = mfma32<T>(fr[i % (PF + 1)], pf[n >> 2], oacc[n & 3]);
+      }
+    }
+  };
+
+  // Softmax of S(t) into P(t) (packed 16-bit), online max / sum with lazy rescale.
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const int t0 = t * PBN;
+    const bool need_mask = CAUSAL ? (t0 + PBN - 1 > wpos0) : (t0 + PBN > kv_end);
+    if (need_mask) {
+      // Key t0 + 4hf + c (c a compile-time constant below 64) is masked when it lies
+      // past `lim`, i.e. when c > lim - t0 - 4hf.
+      const int rel = (CAUSAL ? qpos : kv_end - 1) - t0 - 4 * hf;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cr = kt * 32 + 8 * (r >> 2) + (r & 3);
+          sacc[kt][r] = cr > rel ? -INFINITY : sacc[kt][r];
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+    mx = fmaxf(mx, partner32(mx)) * c;
+    const float m_old = m_use;
+    const float m_new = (mx > m_old + kLazyRescalePP) ? mx : m_old;
+    m_use = m_new;
+    if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {
+      const float alpha = fast_exp2(m_old - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+    }
+    float ls = l_run;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -m_new));
+        const float p1 = fast_exp2(__builtin_fmaf(sacc[kt][r + 1], c, -m_new));
+        const uint32_t pk = pack2<T>(p0, p1);
+        pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
+        ls = sum_pair<T>(pk, ls);
+      }
+    l_run = ls;
+  };
+
+  // Step bookkeeping shared by both groups: at the start of even step k >= 2 issue
+  // stage k/2 + 2; at the end of odd step k wait for stage (k+1)/2 (the next stage may
+  // stay in flight) and publish it with the barrier.
+  const int last_step = 2 * n_tiles + 1;
+  auto step_begin = [&](int k) __attribute__((always_inline)) {
+    if (!(k & 1) && k >= 2) {
+      const int u = k / 2 + 2;
+      if (u <= n_tiles) issue_stage(u);
+    }
+  };
+  auto step_end = [&](int k) __attribute__((always_inline)) {
+    if (k & 1) {
+      const int u = (k + 1) / 2;
+      if (u + 1 <= n_tiles) wait_vmcnt<4>();
+      else wait_vmcnt<0>();
+    }
+    if (k < last_step) step_barrier();
+  };
+
+  int k = 0;
+  if (grp == 1) {  // group 1 starts one step late
+    step_begin(k);
+    step_end(k);
+    ++k;
+  }
+  step_begin(k);
+  qk0();
+  step_end(k);
+  ++k;
+  step_begin(k);
+  softmax(0);
+  step_end(k);
+  ++k;
+  // Tile t's MFMA phase reads ring slot (t+1) % 3; the loop is unrolled by three so
+  // every LDS offset is a compile-time constant.  Tiles before the last one always run
+  // the QK product of the next tile, also for a wave whose queries all precede it: one
+  // MFMA-phase shape inside the loop keeps the accumulators in fixed registers.
+  auto tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
+    step_begin(k);
+    __builtin_amdgcn_s_setprio(1);
+    if (active(t)) mphase(slot_tag, std::true_type{});
+    __builtin_amdgcn_s_setprio(0);
+    step_end(k);
+    ++k;
+    step_begin(k);
+    if (active(t + 1)) softmax(t + 1);
+    step_end(k);
+    ++k;
+  };
+  const int n_loop = n_tiles - 1;
+  for (int t = 0; t < n_loop; t += 3) {
+    tile(t, std::integral_constant<int, 1>{});
+    if (t + 1 < n_loop) tile(t + 1, std::integral_constant<int, 2>{});
+    if (t + 2 < n_loop) tile(t + 2, std::integral_constant<int, 0>{});
+  }
+  {  // last tile: PV only
+    const int t = n_loop;
+    step_begin(k);
+    __builtin_amdgcn_s_setprio(1);
+    if (active(t)) {
+      switch ((t + 1) % PSTAGES) {
+        case 0: mphase(std::integral_constant<int, 0>{}, std::false_type{}); break;
+        case 1: mphase(std::integral_constant<int, 1>{}, std::false_type{}); break;
+        default: mphase(std::integral_constant<int, 2>{}, std::false_type{}); break;
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    step_end(k);
+    ++k;
+  }
+  if (grp == 0) {  // group 0 ends one step early
+    step_begin(k);
+    step_end(k);
+    ++k;
+  }
+
+  // ------------------------------------------------------------ normalise and store
+  const float inv = 1.f / (l_run + partner32(l_run));
+  if (qi < q_n) {
+    T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
+            (long)head * a.o_head_stride;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int d0 = t * 32 + 8 * rg + 4 * hf;
+        u32x2 pk = {pack2<T>(oacc[t][4 * rg] * inv, oacc[t][4 * rg + 1] * inv),
+                    pack2<T>(oacc[t][4 * rg + 2] * inv, oacc[t][4 * rg + 3] * inv)};
+        *reinterpret_cast<u32x2*>(op + d0) = pk;
+      }
+  }
+}
+
+template <typename T, bool CAUSAL>
+hipError_t launch_pp_t(const FwdArgs& a, hipStream_t stream) {
+  long blocks;
+  if (CAUSAL) blocks = (long)((a.n_q + PBM - 1) / PBM) * a.Hq;
+  else blocks = (long)a.n_seg * ((a.max_seqlen + PBM - 1) / PBM) * a.Hq;
+  if (blocks <= 0) return hipSuccess;
+  static unsigned long long configured = 0;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 64 || !(__atomic_load_n(&configured, __ATOMIC_ACQUIRE) & (1ull << dev))) {
+    e = hipFuncSetAttribute((const void*)fwd_pp_kernel<T, CAUSAL>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, PLDS_BYTES);
+    if (e != hipSuccess) return e;
+    if (dev < 64) __atomic_fetch_or(&configured, 1ull << dev, __ATOMIC_RELEASE);
+  }
+  hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL>), dim3((unsigned)blocks), dim3(PTHREADS),
+                     PLDS_BYTES, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool fwd_pp_supports(const FwdArgs& a, int dtype) {
+  if (a.head_size != PD || !(dtype == kF16 || dtype == kBF16)) return false;
+  // K/V rows and Q/O rows are read as 16-byte chunks.
+  return a.kv_tok_stride % 8 == 0 && a.kv_head_stride % 8 == 0 && a.q_tok_stride % 8 == 0 &&
+         a.q_head_stride % 8 == 0;
+}
+
+hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream) {
+  if (dtype == kF16)
+    return causal ? launch_pp_t<f16, true>(a, stream) : launch_pp_t<f16, false>(a, stream);
+  return causal ? launch_pp_t<bf16, true>(a, stream) : launch_pp_t<bf16, false>(a, stream);
+}
+
+}  // namespace orin

@@ -60,4 +60,8 @@ bool fwd_supports(int dtype, int head_size);
 hipError_t launch_fwd_causal(const FwdArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_fwd_varlen(const FwdArgs& a, int dtype, hipStream_t stream);
 
+// 8-wave ping-pong variant for head size 128 (fwd_pp.hip).
+bool fwd_pp_supports(const FwdArgs& a, int dtype);
+hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream);
+
 }  // namespace orin
