@@ -42,6 +42,7 @@
 #include "kernels.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 namespace orin {
 
@@ -468,13 +469,17 @@ hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
-// The ping-pong kernel (256-query workgroups, one per CU) takes head size 128 when its
-// grid covers every CU at least once.
+// Head size 128 goes to the ping-pong kernel (256-query workgroups, one per CU) when its
+// grid covers every CU at least once.  ORIN_FWD_KERNEL=tile|pp overrides the choice (for
+// measurements and tests); unset or any other value keeps it.
 template <bool CAUSAL>
 bool use_pp(const FwdArgs& a, int dtype) {
   static const int mode = [] {
-    const char* e = getenv("ORIN_FWD_PP");
-    return e ? atoi(e) : -1;
+    const char* e = getenv("ORIN_FWD_KERNEL");
+    if (!e) return -1;
+    if (!strcmp(e, "tile")) return 0;
+    if (!strcmp(e, "pp")) return 1;
+    return -1;
   }();
   if (mode == 0 || !fwd_pp_supports(a, dtype)) return false;
   if (mode == 1) return true;

@@ -1,0 +1,54 @@
+"""GPU parity of the 8-wave ping-pong MFMA kernel (head size 128, grids of at least 256
+256-query workgroups, which it is picked for) against the oracle: ragged causal lengths,
+start_pos > 0, output aliasing query, and bidirectional varlen segments."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from orinmllm_amd import kernel as K
+from tests.test_gpu_prefill import run_prefill, sample_rows
+from tests.test_gpu_vision import TORCH, dev, vision_inputs
+from tests.util import assert_lowp_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("start_pos,S", [(0, 2000), (300, 1900), (0, 2049)])
+def test_pp_causal_ragged_prefix(kind, start_pos, S):
+    """32 q / 8 kv heads, S not a multiple of the 256-row workgroup or 64-key tile; the
+    last workgroup's rows past S are never stored."""
+    rng = np.random.default_rng(start_pos + S)
+    Hq, Hkv, d = 32, 8, 128
+    q, kc, vc, out = run_prefill(kind, start_pos, S, Hq, Hkv, d, start_pos + S + 64, 2, 1, rng)
+    rows = sample_rows(S, 40, rng)
+    ref = oracle.prefill_causal(start_pos, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
+    assert_lowp_close(out[rows], ref, what=f"pp {kind} start {start_pos} S {S}")
+
+
+def test_pp_output_aliases_query():
+    rng = np.random.default_rng(7)
+    S, Hq, Hkv, d = 2048, 32, 4, 128
+    q, kc, vc, out = run_prefill("fp16", 0, S, Hq, Hkv, d, S, 1, 0, rng, alias=True)
+    rows = sample_rows(S, 40, rng)
+    ref = oracle.prefill_causal(0, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
+    assert_lowp_close(out[rows], ref, what="pp aliased")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+def test_pp_varlen_bidirectional(kind):
+    """4 segments (one ragged) x 16 heads, d 128: 256 workgroups of 256 queries."""
+    rng = np.random.default_rng(11)
+    H, d = 16, 128
+    cu = np.array([0, 1024, 2048, 2900, 3924], np.int32)
+    q, k, v = vision_inputs(rng, cu, H, d, kind)
+    N = int(cu[-1])
+    out = torch.zeros(N, H * d, device="cuda", dtype=TORCH[kind])
+    K.vision_attention_varlen_cu(dev(q, kind), dev(k, kind), dev(v, kind), out,
+                                 torch.from_numpy(cu).cuda(), 1024, H, d)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([[0, 1023, 1024, 2047, 2048, 2899, 2900, N - 1],
+                                     rng.integers(0, N, 48)]))
+    ref = oracle.varlen_bidir(q, k, v, cu, rows=rows, nthreads=8)
+    assert_lowp_close(out.float().cpu().numpy()[rows], ref, what=f"pp varlen {kind}")
