@@ -213,6 +213,90 @@ int orin_vision_attention_varlen(const void* q, const void* k, const void* v, vo
                                  int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                  float softmax_scale, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------ KV-cache writes */
+
+/*
+ * kernel::copy_to_kv_cache_kernel / copy_to_kv_cache_kernel_fp16
+ * (kuiper/source/op/kernels/cuda/kv_cache_kernel.cuh:24-33, kv_cache_kernel.cu:43-57):
+ * kv_cache[layer_idx][*pos][0..kv_dim) = src[0..kv_dim) for a kuiper cache
+ * [layers, seq_len, kv_dim].  The position is read from device memory when the kernel
+ * runs, so a captured graph can be replayed with a new position.  fp32 / fp16 / bf16.
+ */
+int orin_copy_to_kv_cache(void* kv_cache, const void* src, const int32_t* pos, int32_t kv_dim,
+                          int32_t layer_idx, int32_t seq_len, int32_t dtype, void* stream);
+
+/*
+ * Paged-cache write (no reference function: the reference's contiguous prefill copy is
+ * the cudaMemcpyAsync pair of kuiper/source/model/qwen3.cpp:1220-1241).  Row r of k_src
+ * and v_src ([n_rows, kv_head_num*head_size], row stride src_row_stride elements) is
+ * stored at pool slot slot_mapping[r] (device int32: block * block_size + offset within
+ * the block; a negative slot skips the row).  Pools use the layouts of
+ * orin_attn_decode_paged (kv_layout).  head_size*sizeof(element) and src_row_stride
+ * must be multiples of 16 bytes.
+ */
+int orin_kv_cache_write_paged(const void* k_src, const void* v_src, int64_t src_row_stride,
+                              void* k_pool, void* v_pool, const int32_t* slot_mapping,
+                              int32_t n_rows, int32_t kv_head_num, int32_t head_size,
+                              int32_t block_size, int32_t kv_layout, int32_t dtype,
+                              void* stream);
+
+/*
+ * Copy tokens [0, n_tokens) of one sequence between a contiguous cache
+ * [n_tokens, kv_head_num*head_size] (row stride contig_row_stride elements, e.g. one
+ * kuiper layer) and a paged pool through the sequence's block table (device int32).
+ * direction ORIN_KV_TO_PAGED or ORIN_KV_TO_CONTIGUOUS.  No reference function.
+ */
+#define ORIN_KV_TO_PAGED 0
+#define ORIN_KV_TO_CONTIGUOUS 1
+int orin_kv_cache_convert(void* contig, int64_t contig_row_stride, void* pool,
+                          const int32_t* block_table, int32_t n_tokens, int32_t kv_head_num,
+                          int32_t head_size, int32_t block_size, int32_t kv_layout,
+                          int32_t direction, int32_t dtype, void* stream);
+
+/* ------------------------------------------------------------------ Q/K producers */
+
+/*
+ * kernel::sin_cos_cache_calc_cu (kuiper/source/op/kernels/cuda/rope_kernel.cu:86-98,
+ * 153-166): sin_cache/cos_cache [max_seq_len, head_size] fp32 with entry [p][i] =
+ * sin/cos(p * theta^(-i/head_size)) (the reference uses theta = 1e6).
+ */
+int orin_rope_sin_cos_cache(float* sin_cache, float* cos_cache, int32_t head_size,
+                            int32_t max_seq_len, float theta, void* stream);
+
+/*
+ * The Qwen3 attention producer in one pass (replaces kernel::rmsnorm_kernel_cu_dim on
+ * the q and k heads, rmsnorm_kernel.cu:483-545, then kernel::batched_rope_kernel_cu /
+ * rope_kernel_cu_gpu_pos, rope_kernel.cu:377-427, 464-509, then the two cache copies of
+ * kuiper/source/model/qwen3.cpp:1195-1241).  For tokens t < seq_len at positions
+ * p = start + t (start = *pos_ptr if pos_ptr is non-NULL, else start_pos):
+ *   query[t, h] <- rope(rmsnorm(query[t, h]) * q_norm_weight)         (in place)
+ *   key_cache[layer][p][g] <- rope(rmsnorm(key[t, g]) * k_norm_weight)
+ *   value_cache[layer][p][g] <- value[t, g]
+ * rmsnorm(x) = x / sqrt(mean(x^2) + eps) in fp32; rope rotates pairs (j, j + d/2) with
+ * sin_cache/cos_cache[p][2j].  A NULL weight skips that normalisation (Qwen2 / Llama).
+ * head_size 128 or 256; fp32 / fp16 / bf16 (weights in the same type).
+ */
+int orin_qk_norm_rope(void* query, const void* key, const void* value,
+                      const void* q_norm_weight, const void* k_norm_weight,
+                      const float* sin_cache, const float* cos_cache, void* key_cache,
+                      void* value_cache, int32_t layer_index, int32_t max_seq_len,
+                      int32_t start_pos, const int32_t* pos_ptr, int32_t seq_len,
+                      int32_t head_num, int32_t kv_head_num, int32_t head_size, float eps,
+                      int32_t dtype, void* stream);
+
+/*
+ * kernel::fused_split_rope_transpose_cu
+ * (kuiper/source/op/kernels/cuda/vision_encoder_kernel.cu:662-773): qkv
+ * [num_tokens, 3*num_heads*head_dim] -> q_trans/k_trans/v_trans [num_heads, num_tokens,
+ * head_dim], with the 2-D rotary x1' = x1*cos[j] - x2*sin[j],
+ * x2' = x1*sin[j+d/2] + x2*cos[j+d/2] (cos/sin [num_tokens, head_dim], same type) on
+ * q and k.  fp16 / bf16 / fp32.
+ */
+int orin_vision_split_rope_transpose(const void* qkv, const void* cos_cache,
+                                     const void* sin_cache, void* q_trans, void* k_trans,
+                                     void* v_trans, int32_t num_tokens, int32_t num_heads,
+                                     int32_t head_dim, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

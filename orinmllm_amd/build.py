@@ -18,7 +18,7 @@ REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborin_attn.so")
-SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "capi.hip"]
+SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "capi.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -569,4 +569,108 @@ int orin_vision_attention_varlen(const void* q, const void* k, const void* v, vo
                        head_dim, softmax_scale, dtype, stream);
 }
 
+
+// ------------------------------------------------------------------ KV-cache writes
+
+static bool dtype_ok(int32_t dtype) {
+  return dtype == ORIN_DTYPE_FP32 || dtype == ORIN_DTYPE_FP16 || dtype == ORIN_DTYPE_BF16;
+}
+static int elem_bytes(int32_t dtype) { return dtype == ORIN_DTYPE_FP32 ? 4 : 2; }
+
+int orin_copy_to_kv_cache(void* kv_cache, const void* src, const int32_t* pos, int32_t kv_dim,
+                          int32_t layer_idx, int32_t seq_len, int32_t dtype, void* stream) {
+  if (!kv_cache || !src || !pos || kv_dim <= 0 || layer_idx < 0 || seq_len <= 0)
+    return ORIN_ERR_INVALID_ARG;
+  if (!dtype_ok(dtype)) return ORIN_ERR_UNSUPPORTED;
+  return hip_status(launch_kv_append(kv_cache, src, pos, kv_dim,
+                                     (long)layer_idx * seq_len * kv_dim, dtype,
+                                     (hipStream_t)stream));
+}
+
+int orin_kv_cache_write_paged(const void* k_src, const void* v_src, int64_t src_row_stride,
+                              void* k_pool, void* v_pool, const int32_t* slot_mapping,
+                              int32_t n_rows, int32_t kv_head_num, int32_t head_size,
+                              int32_t block_size, int32_t kv_layout, int32_t dtype,
+                              void* stream) {
+  if (!k_src || !v_src || !k_pool || !v_pool || !slot_mapping || n_rows < 0 ||
+      kv_head_num <= 0 || head_size <= 0 || block_size <= 0 ||
+      src_row_stride < (int64_t)kv_head_num * head_size)
+    return ORIN_ERR_INVALID_ARG;
+  if (kv_layout != ORIN_KV_LAYOUT_TOKEN_MAJOR && kv_layout != ORIN_KV_LAYOUT_HEAD_MAJOR)
+    return ORIN_ERR_INVALID_ARG;
+  if (!dtype_ok(dtype)) return ORIN_ERR_UNSUPPORTED;
+  const int vec = 16 / elem_bytes(dtype);
+  if (head_size % vec || src_row_stride % vec) return ORIN_ERR_UNSUPPORTED;
+  return hip_status(launch_kv_scatter(k_src, v_src, k_pool, v_pool, slot_mapping,
+                                      src_row_stride, n_rows, kv_head_num, head_size, block_size,
+                                      kv_layout == ORIN_KV_LAYOUT_HEAD_MAJOR, dtype,
+                                      (hipStream_t)stream));
+}
+
+int orin_kv_cache_convert(void* contig, int64_t contig_row_stride, void* pool,
+                          const int32_t* block_table, int32_t n_tokens, int32_t kv_head_num,
+                          int32_t head_size, int32_t block_size, int32_t kv_layout,
+                          int32_t direction, int32_t dtype, void* stream) {
+  if (!contig || !pool || !block_table || n_tokens < 0 || kv_head_num <= 0 || head_size <= 0 ||
+      block_size <= 0 || contig_row_stride < (int64_t)kv_head_num * head_size)
+    return ORIN_ERR_INVALID_ARG;
+  if (kv_layout != ORIN_KV_LAYOUT_TOKEN_MAJOR && kv_layout != ORIN_KV_LAYOUT_HEAD_MAJOR)
+    return ORIN_ERR_INVALID_ARG;
+  if (direction != ORIN_KV_TO_PAGED && direction != ORIN_KV_TO_CONTIGUOUS)
+    return ORIN_ERR_INVALID_ARG;
+  if (!dtype_ok(dtype)) return ORIN_ERR_UNSUPPORTED;
+  const int vec = 16 / elem_bytes(dtype);
+  if (head_size % vec || contig_row_stride % vec) return ORIN_ERR_UNSUPPORTED;
+  return hip_status(launch_kv_convert(contig, pool, block_table, contig_row_stride, n_tokens,
+                                      kv_head_num, head_size, block_size,
+                                      kv_layout == ORIN_KV_LAYOUT_HEAD_MAJOR,
+                                      direction == ORIN_KV_TO_PAGED, dtype, (hipStream_t)stream));
+}
+
+// ------------------------------------------------------------------ Q/K producers
+
+int orin_rope_sin_cos_cache(float* sin_cache, float* cos_cache, int32_t head_size,
+                            int32_t max_seq_len, float theta, void* stream) {
+  if (!sin_cache || !cos_cache || head_size <= 0 || max_seq_len <= 0 || !(theta > 0.f))
+    return ORIN_ERR_INVALID_ARG;
+  return hip_status(
+      launch_rope_cache(sin_cache, cos_cache, head_size, max_seq_len, theta, (hipStream_t)stream));
+}
+
+int orin_qk_norm_rope(void* query, const void* key, const void* value,
+                      const void* q_norm_weight, const void* k_norm_weight,
+                      const float* sin_cache, const float* cos_cache, void* key_cache,
+                      void* value_cache, int32_t layer_index, int32_t max_seq_len,
+                      int32_t start_pos, const int32_t* pos_ptr, int32_t seq_len,
+                      int32_t head_num, int32_t kv_head_num, int32_t head_size, float eps,
+                      int32_t dtype, void* stream) {
+  if (!query || !key || !value || !sin_cache || !cos_cache || !key_cache || !value_cache)
+    return ORIN_ERR_INVALID_ARG;
+  if (seq_len <= 0 || head_num <= 0 || kv_head_num <= 0 || head_size <= 0 || layer_index < 0 ||
+      max_seq_len <= 0 || start_pos < 0 || !(eps >= 0.f))
+    return ORIN_ERR_INVALID_ARG;
+  if (!pos_ptr && start_pos + seq_len > max_seq_len) return ORIN_ERR_INVALID_ARG;
+  if (!norm_rope_supports(dtype, head_size)) return ORIN_ERR_UNSUPPORTED;
+  const long kv_dim = (long)kv_head_num * head_size;
+  const long layer_off = (long)layer_index * max_seq_len * kv_dim * elem_bytes(dtype);
+  return hip_status(launch_qk_norm_rope(
+      query, key, value, q_norm_weight, k_norm_weight, sin_cache, cos_cache,
+      static_cast<char*>(key_cache) + layer_off, static_cast<char*>(value_cache) + layer_off,
+      kv_dim, pos_ptr, start_pos, seq_len, head_num, kv_head_num, head_size, eps, dtype,
+      (hipStream_t)stream));
+}
+
+int orin_vision_split_rope_transpose(const void* qkv, const void* cos_cache,
+                                     const void* sin_cache, void* q_trans, void* k_trans,
+                                     void* v_trans, int32_t num_tokens, int32_t num_heads,
+                                     int32_t head_dim, int32_t dtype, void* stream) {
+  if (!qkv || !cos_cache || !sin_cache || !q_trans || !k_trans || !v_trans || num_tokens <= 0 ||
+      num_heads <= 0 || head_dim <= 0 || head_dim % 2)
+    return ORIN_ERR_INVALID_ARG;
+  if (!dtype_ok(dtype)) return ORIN_ERR_UNSUPPORTED;
+  return hip_status(launch_vision_qkv(qkv, cos_cache, sin_cache, q_trans, k_trans, v_trans,
+                                      num_tokens, num_heads, head_dim, dtype,
+                                      (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -64,4 +64,27 @@ hipError_t launch_fwd_varlen(const FwdArgs& a, int dtype, hipStream_t stream);
 bool fwd_pp_supports(const FwdArgs& a, int dtype);
 hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream);
 
+// KV-cache writes and Q/K producers (producers.hip).
+hipError_t launch_kv_append(void* cache, const void* src, const int* pos, int kv_dim,
+                            long layer_off, int dtype, hipStream_t stream);
+hipError_t launch_kv_scatter(const void* k_src, const void* v_src, void* k_pool, void* v_pool,
+                             const int* slots, long src_row_stride, int n_rows, int kv_heads,
+                             int head_size, int block_size, int head_major, int dtype,
+                             hipStream_t stream);
+hipError_t launch_kv_convert(void* contig, void* pool, const int* block_table,
+                             long contig_row_stride, int n_tokens, int kv_heads, int head_size,
+                             int block_size, int head_major, int to_paged, int dtype,
+                             hipStream_t stream);
+bool norm_rope_supports(int dtype, int head_size);
+hipError_t launch_qk_norm_rope(void* q, const void* k, const void* v, const void* q_weight,
+                               const void* k_weight, const float* sin_cache,
+                               const float* cos_cache, void* k_cache, void* v_cache,
+                               long cache_tok_stride, const int* pos_ptr, int start_pos,
+                               int seq_len, int Hq, int Hkv, int head_size, float eps, int dtype,
+                               hipStream_t stream);
+hipError_t launch_rope_cache(float* sin_cache, float* cos_cache, int head_size, int max_pos,
+                             float theta, hipStream_t stream);
+hipError_t launch_vision_qkv(const void* qkv, const void* cos_t, const void* sin_t, void* q,
+                             void* k, void* v, int N, int H, int d, int dtype, hipStream_t stream);
+
 }  // namespace orin

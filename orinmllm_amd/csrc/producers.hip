@@ -1,0 +1,358 @@
+// The kernels either side of the attention hot path on gfx950: KV-cache writes and the
+// Q/K producers.  All of them are HBM-bound element moves with a little fp32 math, so
+// each workgroup streams 16-byte chunks with coalesced, vectorised loads and stores.
+//
+//  kv_append_kernel        kernel::copy_to_kv_cache_kernel{,_fp16}
+//                          (kuiper/source/op/kernels/cuda/kv_cache_kernel.cu:13-57): one
+//                          token's K or V row into a kuiper cache [layers, max_seq, kv_dim]
+//                          at a position read from device memory (graph-capturable).
+//  kv_scatter_kernel       rows of K and V into a paged pool through a slot mapping
+//                          (the paged-cache counterpart of the cudaMemcpyAsync pair of
+//                          qwen3.cpp:1220-1241).
+//  kv_convert_kernel       one sequence between a contiguous kuiper layer cache and a
+//                          paged pool (either direction).
+//  qk_norm_rope_kernel     per-head RMSNorm (rmsnorm_kernel.cu:483-545, eps 1e-6) then
+//                          rotate-half RoPE (rope_kernel.cu:464-509, sin/cos cache entry
+//                          2j for pair (j, j+d/2)) of Q in place and of K, with the rotated
+//                          K and the V rows written to the cache -- the rmsnorm x2 +
+//                          batched_rope + two cudaMemcpyAsync of qwen3.cpp:1195-1241 in
+//                          one pass.
+//  vision_qkv_kernel       kernel::fused_split_rope_transpose_cu
+//                          (vision_encoder_kernel.cu:662-773): split [N, 3*H*d] into
+//                          head-major q/k/v [H, N, d] with the 2-D rotary on q and k.
+#include "common.h"
+#include "kernels.h"
+
+namespace orin {
+
+namespace {
+
+constexpr int kProdThreads = 256;
+
+// 16-byte copy of element range [i, i+VEC) when the row is 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void copy16(T* dst, const T* src) {
+  *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+}
+
+// ---------------------------------------------------------------- kuiper append
+template <typename T>
+__global__ void __launch_bounds__(kProdThreads)
+kv_append_kernel(T* cache, const T* src, const int* pos, int kv_dim, long layer_off) {
+  const int position = *reinterpret_cast<const volatile int*>(pos);
+  T* dst = cache + layer_off + (long)position * kv_dim;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int i = (blockIdx.x * kProdThreads + threadIdx.x) * VEC;
+  if (kv_dim % VEC == 0) {
+    if (i < kv_dim) copy16(dst + i, src + i);
+  } else {
+    for (int e = i; e < min(i + VEC, kv_dim); ++e) dst[e] = src[e];
+  }
+}
+
+// ---------------------------------------------------------------- paged scatter
+// Row r of k_src / v_src (row_elems = kv_heads * head_size elements) goes to pool slot
+// slots[r] (block slots[r] / block_size, offset slots[r] % block_size); a negative slot
+// skips the row.  Token-major pool: [blocks, block_size, kv_heads, head_size]; head-major:
+// [blocks, kv_heads, block_size, head_size].  One 16-byte chunk per thread.
+struct ScatterArgs {
+  const void* k_src;
+  const void* v_src;
+  void* k_pool;
+  void* v_pool;
+  const int* slots;
+  long src_row_stride;  // elements between source rows
+  int n_rows, kv_heads, head_size, block_size, head_major;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kProdThreads) kv_scatter_kernel(ScatterArgs a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int chunks_per_head = a.head_size / VEC;
+  const int chunks_per_row = a.kv_heads * chunks_per_head;
+  const long idx = (long)blockIdx.x * kProdThreads + threadIdx.x;
+  const int r = (int)(idx / chunks_per_row);
+  if (r >= a.n_rows) return;
+  const int c = (int)(idx % chunks_per_row);
+  const int slot = a.slots[r];
+  if (slot < 0) return;
+  const int h = c / chunks_per_head, e = (c % chunks_per_head) * VEC;
+  const long blk = slot / a.block_size, off = slot % a.block_size;
+  const long dst = a.head_major
+                       ? ((blk * a.kv_heads + h) * a.block_size + off) * a.head_size + e
+                       : ((blk * a.block_size + off) * a.kv_heads + h) * a.head_size + e;
+  const long src = (long)r * a.src_row_stride + (long)h * a.head_size + e;
+  copy16(reinterpret_cast<T*>(a.k_pool) + dst, reinterpret_cast<const T*>(a.k_src) + src);
+  copy16(reinterpret_cast<T*>(a.v_pool) + dst, reinterpret_cast<const T*>(a.v_src) + src);
+}
+
+// ---------------------------------------------------------------- contiguous <-> paged
+// Tokens [0, n_tokens) of one sequence: contiguous cache rows [n, kv_heads * head_size]
+// and pool blocks block_table[t / block_size].  to_paged selects the direction.
+struct ConvertArgs {
+  void* contig;
+  void* pool;
+  const int* block_table;
+  long contig_row_stride;
+  int n_tokens, kv_heads, head_size, block_size, head_major, to_paged;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kProdThreads) kv_convert_kernel(ConvertArgs a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int chunks_per_head = a.head_size / VEC;
+  const int chunks_per_row = a.kv_heads * chunks_per_head;
+  const long idx = (long)blockIdx.x * kProdThreads + threadIdx.x;
+  const int t = (int)(idx / chunks_per_row);
+  if (t >= a.n_tokens) return;
+  const int c = (int)(idx % chunks_per_row);
+  const int h = c / chunks_per_head, e = (c % chunks_per_head) * VEC;
+  const long blk = a.block_table[t / a.block_size], off = t % a.block_size;
+  const long p = a.head_major ? ((blk * a.kv_heads + h) * a.block_size + off) * a.head_size + e
+                              : ((blk * a.block_size + off) * a.kv_heads + h) * a.head_size + e;
+  const long q = (long)t * a.contig_row_stride + (long)h * a.head_size + e;
+  T* pool = reinterpret_cast<T*>(a.pool);
+  T* contig = reinterpret_cast<T*>(a.contig);
+  if (a.to_paged) copy16(pool + p, contig + q);
+  else copy16(contig + q, pool + p);
+}
+
+// ---------------------------------------------------------------- Q/K norm + RoPE
+// One wave per (token, head) unit: lane j owns the RoPE pairs (j + 64i, j + 64i + d/2).
+// Units 0..Hq-1 of a token are its query heads (rotated in place), units Hq..Hq+Hkv-1
+// its key heads (rotated, written to the K cache) -- each key unit also copies the
+// token's V head row to the V cache.
+struct NormRopeArgs {
+  void* q;                 // [S, Hq * d], in place
+  const void* k;           // [S, Hkv * d]
+  const void* v;           // [S, Hkv * d]
+  const void* q_weight;    // [d] RMSNorm weights (T), null = no norm of Q
+  const void* k_weight;    // [d], null = no norm of K
+  const float* sin_cache;  // [max_pos, d] fp32; entry 2j rotates pair j
+  const float* cos_cache;
+  void* k_cache;           // row of token t: k_cache + (start + t) * cache_tok_stride
+  void* v_cache;
+  long cache_tok_stride;
+  const int* pos_ptr;      // non-null: start position read from device memory
+  int start_pos, seq_len, Hq, Hkv, head_size;
+  float eps;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs a) {
+  constexpr int PAIRS = D / 2 / kWave;  // RoPE pairs per lane
+  static_assert(PAIRS >= 1 && D % (2 * kWave) == 0, "head size must be a multiple of 128");
+  const int lane = threadIdx.x & 63;
+  const long unit = (long)blockIdx.x * (kProdThreads / kWave) + (threadIdx.x >> 6);
+  const int units = a.Hq + a.Hkv;
+  const int t = (int)(unit / units);
+  if (t >= a.seq_len) return;
+  const int u = (int)(unit % units);
+  const bool is_q = u < a.Hq;
+  const int h = is_q ? u : u - a.Hq;
+  const int start = a.pos_ptr ? *a.pos_ptr : a.start_pos;
+  const int pos = start + t;
+
+  const T* x = is_q ? reinterpret_cast<const T*>(a.q) + ((long)t * a.Hq + h) * D
+                    : reinterpret_cast<const T*>(a.k) + ((long)t * a.Hkv + h) * D;
+  float lo[PAIRS], hi[PAIRS];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) {
+    const int j = lane + kWave * i;
+    lo[i] = to_f32(x[j]);
+    hi[i] = to_f32(x[j + D / 2]);
+    ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
+  }
+  const T* w = reinterpret_cast<const T*>(is_q ? a.q_weight : a.k_weight);
+  if (w) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) ss += shfl_xor_f(ss, m);
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+      const int j = lane + kWave * i;
+      lo[i] = lo[i] * inv * to_f32(w[j]);
+      hi[i] = hi[i] * inv * to_f32(w[j + D / 2]);
+    }
+  }
+  T* out = is_q ? reinterpret_cast<T*>(a.q) + ((long)t * a.Hq + h) * D
+                : reinterpret_cast<T*>(a.k_cache) + (long)pos * a.cache_tok_stride + (long)h * D;
+  const float* sn = a.sin_cache + (long)pos * D;
+  const float* cs = a.cos_cache + (long)pos * D;
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) {
+    const int j = lane + kWave * i;
+    const float s = sn[2 * j], c = cs[2 * j];
+    out[j] = from_f32<T>(c * lo[i] - s * hi[i]);
+    out[j + D / 2] = from_f32<T>(c * hi[i] + s * lo[i]);
+  }
+  if (!is_q) {
+    const T* vr = reinterpret_cast<const T*>(a.v) + ((long)t * a.Hkv + h) * D;
+    T* vo = reinterpret_cast<T*>(a.v_cache) + (long)pos * a.cache_tok_stride + (long)h * D;
+#pragma unroll
+    for (int i = 0; i < 2 * PAIRS; ++i) vo[lane + kWave * i] = vr[lane + kWave * i];
+  }
+}
+
+// sin/cos cache of rope_kernel.cu:86-98 / 153-166: entry [p][i] = sin/cos(p * theta^(-i/d)).
+__global__ void __launch_bounds__(kProdThreads)
+rope_cache_kernel(float* sin_cache, float* cos_cache, int head_size, int max_pos, float theta) {
+  const long idx = (long)blockIdx.x * kProdThreads + threadIdx.x;
+  if (idx >= (long)head_size * max_pos) return;
+  const int i = (int)(idx % head_size);
+  const int p = (int)(idx / head_size);
+  const float freq = 1.0f / powf(theta, (float)i / (float)head_size);
+  float s, c;
+  sincosf((float)p * freq, &s, &c);
+  sin_cache[idx] = s;
+  cos_cache[idx] = c;
+}
+
+// ---------------------------------------------------------------- vision split + rotary
+// qkv [N, 3 * H * d] (q | k | v per token) -> head-major q/k/v [H, N, d]; q and k get
+// x1' = x1 cos[j] - x2 sin[j], x2' = x1 sin[j + d/2] + x2 cos[j + d/2] with the
+// [N, d] cos/sin tables in T.  One thread per (token, head, pair j).
+template <typename T>
+__global__ void __launch_bounds__(kProdThreads)
+vision_qkv_kernel(const T* qkv, const T* cos_t, const T* sin_t, T* qo, T* ko, T* vo, int N, int H,
+                  int d) {
+  const int half = d / 2;
+  const long idx = (long)blockIdx.x * kProdThreads + threadIdx.x;
+  if (idx >= (long)N * H * half) return;
+  const int j = (int)(idx % half);
+  const long th = idx / half;
+  const int h = (int)(th % H);
+  const int t = (int)(th / H);
+  const long hidden = (long)H * d;
+  const T* row = qkv + (long)t * 3 * hidden + (long)h * d;
+  const float c1 = to_f32(cos_t[(long)t * d + j]), s1 = to_f32(sin_t[(long)t * d + j]);
+  const float c2 = to_f32(cos_t[(long)t * d + j + half]);
+  const float s2 = to_f32(sin_t[(long)t * d + j + half]);
+  const long o = ((long)h * N + t) * d;
+  {
+    const float x1 = to_f32(row[j]), x2 = to_f32(row[j + half]);
+    qo[o + j] = from_f32<T>(__builtin_fmaf(x1, c1, -(x2 * s1)));
+    qo[o + j + half] = from_f32<T>(__builtin_fmaf(x1, s2, x2 * c2));
+  }
+  {
+    const float x1 = to_f32(row[hidden + j]), x2 = to_f32(row[hidden + j + half]);
+    ko[o + j] = from_f32<T>(__builtin_fmaf(x1, c1, -(x2 * s1)));
+    ko[o + j + half] = from_f32<T>(__builtin_fmaf(x1, s2, x2 * c2));
+  }
+  vo[o + j] = row[2 * hidden + j];
+  vo[o + j + half] = row[2 * hidden + j + half];
+}
+
+unsigned grid_for(long items) { return (unsigned)((items + kProdThreads - 1) / kProdThreads); }
+
+template <typename F>
+hipError_t by_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case kF32: return f(float{});
+    case kF16: return f(f16{});
+    case kBF16: return f(bf16{});
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_kv_append(void* cache, const void* src, const int* pos, int kv_dim,
+                            long layer_off, int dtype, hipStream_t stream) {
+  return by_dtype(dtype, [&](auto z) {
+    using T = decltype(z);
+    constexpr int VEC = 16 / (int)sizeof(T);
+    const long chunks = (kv_dim + VEC - 1) / VEC;
+    hipLaunchKernelGGL(kv_append_kernel<T>, dim3(grid_for(chunks)), dim3(kProdThreads), 0, stream,
+                       reinterpret_cast<T*>(cache), reinterpret_cast<const T*>(src), pos, kv_dim,
+                       layer_off);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_kv_scatter(const void* k_src, const void* v_src, void* k_pool, void* v_pool,
+                             const int* slots, long src_row_stride, int n_rows, int kv_heads,
+                             int head_size, int block_size, int head_major, int dtype,
+                             hipStream_t stream) {
+  ScatterArgs a{k_src, v_src, k_pool, v_pool, slots, src_row_stride,
+                n_rows, kv_heads, head_size, block_size, head_major};
+  return by_dtype(dtype, [&](auto z) {
+    using T = decltype(z);
+    const long chunks = (long)n_rows * kv_heads * (head_size / (16 / (int)sizeof(T)));
+    if (chunks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_scatter_kernel<T>, dim3(grid_for(chunks)), dim3(kProdThreads), 0,
+                       stream, a);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_kv_convert(void* contig, void* pool, const int* block_table,
+                             long contig_row_stride, int n_tokens, int kv_heads, int head_size,
+                             int block_size, int head_major, int to_paged, int dtype,
+                             hipStream_t stream) {
+  ConvertArgs a{contig, pool, block_table, contig_row_stride, n_tokens,
+                kv_heads, head_size, block_size, head_major, to_paged};
+  return by_dtype(dtype, [&](auto z) {
+    using T = decltype(z);
+    const long chunks = (long)n_tokens * kv_heads * (head_size / (16 / (int)sizeof(T)));
+    if (chunks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_convert_kernel<T>, dim3(grid_for(chunks)), dim3(kProdThreads), 0,
+                       stream, a);
+    return hipGetLastError();
+  });
+}
+
+bool norm_rope_supports(int dtype, int head_size) {
+  return (dtype == kF32 || dtype == kF16 || dtype == kBF16) &&
+         (head_size == 128 || head_size == 256);
+}
+
+hipError_t launch_qk_norm_rope(void* q, const void* k, const void* v, const void* q_weight,
+                               const void* k_weight, const float* sin_cache,
+                               const float* cos_cache, void* k_cache, void* v_cache,
+                               long cache_tok_stride, const int* pos_ptr, int start_pos,
+                               int seq_len, int Hq, int Hkv, int head_size, float eps, int dtype,
+                               hipStream_t stream) {
+  NormRopeArgs a{q, k, v, q_weight, k_weight, sin_cache, cos_cache, k_cache, v_cache,
+                 cache_tok_stride, pos_ptr, start_pos, seq_len, Hq, Hkv, head_size, eps};
+  const long units = (long)seq_len * (Hq + Hkv);
+  if (units <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((units + kProdThreads / kWave - 1) / (kProdThreads / kWave));
+  return by_dtype(dtype, [&](auto z) {
+    using T = decltype(z);
+    if (head_size == 128)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 128>), dim3(grid), dim3(kProdThreads), 0, stream,
+                         a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 256>), dim3(grid), dim3(kProdThreads), 0, stream,
+                         a);
+    return hipGetLastError();
+  });
+}
+
+hipError_t launch_rope_cache(float* sin_cache, float* cos_cache, int head_size, int max_pos,
+                             float theta, hipStream_t stream) {
+  const long n = (long)head_size * max_pos;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_cache_kernel, dim3(grid_for(n)), dim3(kProdThreads), 0, stream,
+                     sin_cache, cos_cache, head_size, max_pos, theta);
+  return hipGetLastError();
+}
+
+hipError_t launch_vision_qkv(const void* qkv, const void* cos_t, const void* sin_t, void* q,
+                             void* k, void* v, int N, int H, int d, int dtype,
+                             hipStream_t stream) {
+  return by_dtype(dtype, [&](auto z) {
+    using T = decltype(z);
+    const long n = (long)N * H * (d / 2);
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(vision_qkv_kernel<T>, dim3(grid_for(n)), dim3(kProdThreads), 0, stream,
+                       reinterpret_cast<const T*>(qkv), reinterpret_cast<const T*>(cos_t),
+                       reinterpret_cast<const T*>(sin_t), reinterpret_cast<T*>(q),
+                       reinterpret_cast<T*>(k), reinterpret_cast<T*>(v), N, H, d);
+    return hipGetLastError();
+  });
+}
+
+}  // namespace orin

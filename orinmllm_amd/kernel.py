@@ -300,3 +300,93 @@ def vision_attention_varlen_cu(q_trans, k_trans, v_trans, output, cu_seqlens, ma
         _ptr(q_trans, "q"), _ptr(k_trans, "k"), _ptr(v_trans, "v"), _ptr(output, "output"),
         _i32(cu_seqlens, "cu_seqlens"), n_seqs, max_seqlen, num_tokens, num_heads, head_dim,
         float(softmax_scale), dt, _stream(config)))
+
+
+# ---------------------------------------------------------------- KV-cache writes
+
+KV_TO_PAGED = 0
+KV_TO_CONTIGUOUS = 1
+
+
+def copy_to_kv_cache_kernel(kv_cache, src, pos, kv_dim, layer_idx, seq_len, config=None):
+    """kernel::copy_to_kv_cache_kernel / copy_to_kv_cache_kernel_fp16
+    (kuiper/source/op/kernels/cuda/kv_cache_kernel.cuh:24-33): src [kv_dim] goes to row
+    *pos of layer layer_idx of kv_cache [layers, seq_len, kv_dim]; pos is an int32 GPU
+    tensor read when the kernel runs."""
+    dt = _dtype(kv_cache, src)
+    _lib.check("orin_copy_to_kv_cache", _lib.load().orin_copy_to_kv_cache(
+        _ptr(kv_cache, "kv_cache"), _ptr(src, "src"), _i32(pos, "pos"), kv_dim, layer_idx,
+        seq_len, dt, _stream(config)))
+
+
+def kv_cache_write_paged(k_src, v_src, k_pool, v_pool, slot_mapping,
+                         layout=KV_LAYOUT_TOKEN_MAJOR, config=None):
+    """Store rows of k_src / v_src [n, kv_heads, head_size] at pool slots slot_mapping
+    (int32 [n], block * block_size + offset; negative = skip)."""
+    n, kv_heads, head_size = k_src.shape
+    if layout == KV_LAYOUT_TOKEN_MAJOR:
+        _, block_size, hkv, hs = k_pool.shape
+    else:
+        _, hkv, block_size, hs = k_pool.shape
+    if (hkv, hs) != (kv_heads, head_size) or v_src.shape != k_src.shape:
+        raise ValueError("pool and source shapes disagree")
+    dt = _dtype(k_src, v_src, k_pool, v_pool)
+    _lib.check("orin_kv_cache_write_paged", _lib.load().orin_kv_cache_write_paged(
+        _ptr(k_src, "k_src"), _ptr(v_src, "v_src"), kv_heads * head_size, _ptr(k_pool, "k_pool"),
+        _ptr(v_pool, "v_pool"), _i32(slot_mapping, "slot_mapping"), n, kv_heads, head_size,
+        block_size, layout, dt, _stream(config)))
+
+
+def kv_cache_convert(contig, pool, block_table, n_tokens, direction,
+                     layout=KV_LAYOUT_TOKEN_MAJOR, config=None):
+    """Copy tokens [0, n_tokens) of one sequence between contig [>= n_tokens, kv_heads,
+    head_size] and a paged pool through block_table (int32 [max_blocks])."""
+    _, kv_heads, head_size = contig.shape
+    block_size = pool.shape[1] if layout == KV_LAYOUT_TOKEN_MAJOR else pool.shape[2]
+    dt = _dtype(contig, pool)
+    _lib.check("orin_kv_cache_convert", _lib.load().orin_kv_cache_convert(
+        _ptr(contig, "contig"), kv_heads * head_size, _ptr(pool, "pool"),
+        _i32(block_table, "block_table"), n_tokens, kv_heads, head_size, block_size, layout,
+        direction, dt, _stream(config)))
+
+
+# ---------------------------------------------------------------- Q/K producers
+
+def sin_cos_cache_calc_cu(head_size, max_seq_len, sin_cache, cos_cache, theta=1e6, config=None):
+    """kernel::sin_cos_cache_calc_cu (kuiper/source/op/kernels/cuda/rope_kernel.cu:153-166):
+    fp32 [max_seq_len, head_size] tables, entry [p][i] = sin/cos(p * theta^(-i/head_size))."""
+    if sin_cache.dtype != torch.float32 or cos_cache.dtype != torch.float32:
+        raise ValueError("sin/cos caches are fp32")
+    _lib.check("orin_rope_sin_cos_cache", _lib.load().orin_rope_sin_cos_cache(
+        _ptr(sin_cache, "sin_cache"), _ptr(cos_cache, "cos_cache"), head_size, max_seq_len,
+        float(theta), _stream(config)))
+
+
+def qk_norm_rope_cu(query, key, value, q_norm_weight, k_norm_weight, sin_cache, cos_cache,
+                    key_cache, value_cache, layer_index, max_seq_len, start_pos, seq_len,
+                    head_num, kv_head_num, head_size, eps=1e-6, pos_ptr=None, config=None):
+    """The Qwen3 producer in one pass: per-head RMSNorm + RoPE of query (in place) and key,
+    key and value rows stored at positions start_pos.. of layer layer_index of the kuiper
+    caches.  q/k_norm_weight may be None (no normalisation).  pos_ptr (int32 GPU tensor)
+    replaces start_pos when given."""
+    dt = _dtype(query, key, value, key_cache, value_cache,
+                *[w for w in (q_norm_weight, k_norm_weight) if w is not None])
+    _lib.check("orin_qk_norm_rope", _lib.load().orin_qk_norm_rope(
+        _ptr(query, "query"), _ptr(key, "key"), _ptr(value, "value"),
+        _ptr(q_norm_weight, "q_norm_weight"), _ptr(k_norm_weight, "k_norm_weight"),
+        _ptr(sin_cache, "sin_cache"), _ptr(cos_cache, "cos_cache"), _ptr(key_cache, "key_cache"),
+        _ptr(value_cache, "value_cache"), layer_index, max_seq_len, start_pos,
+        None if pos_ptr is None else _i32(pos_ptr, "pos_ptr"), seq_len, head_num, kv_head_num,
+        head_size, float(eps), dt, _stream(config)))
+
+
+def fused_split_rope_transpose_cu(qkv, cos_cache, sin_cache, q_trans, k_trans, v_trans,
+                                  num_tokens, num_heads, head_dim, config=None):
+    """kernel::fused_split_rope_transpose_cu
+    (kuiper/source/op/kernels/cuda/vision_encoder_kernel.cu:752-773)."""
+    dt = _dtype(qkv, cos_cache, sin_cache, q_trans, k_trans, v_trans)
+    _lib.check("orin_vision_split_rope_transpose",
+               _lib.load().orin_vision_split_rope_transpose(
+                   _ptr(qkv, "qkv"), _ptr(cos_cache, "cos_cache"), _ptr(sin_cache, "sin_cache"),
+                   _ptr(q_trans, "q_trans"), _ptr(k_trans, "k_trans"), _ptr(v_trans, "v_trans"),
+                   num_tokens, num_heads, head_dim, dt, _stream(config)))

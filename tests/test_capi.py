@@ -69,6 +69,36 @@ def test_invalid_arguments_are_rejected():
                                             0.0, _lib.DTYPE_BF16, None) == _lib.ERR_INVALID_ARG
 
 
+def test_producer_arguments_are_rejected():
+    """KV-cache writes and Q/K producers check sizes, layouts and alignment before any
+    launch (no GPU is touched: every call here fails validation)."""
+    lib = _lib.load()
+    F16, INV, UNS = _lib.DTYPE_FP16, _lib.ERR_INVALID_ARG, _lib.ERR_UNSUPPORTED
+    assert lib.orin_copy_to_kv_cache(FAKE, FAKE, None, 1024, 0, 64, F16, None) == INV
+    assert lib.orin_copy_to_kv_cache(FAKE, FAKE, FAKE, 1024, -1, 64, F16, None) == INV
+    assert lib.orin_copy_to_kv_cache(FAKE, FAKE, FAKE, 1024, 0, 64, 9, None) == UNS
+    # paged write: source rows narrower than kv_heads*head_size, bad layout, misaligned head
+    assert lib.orin_kv_cache_write_paged(FAKE, FAKE, 512, FAKE, FAKE, FAKE, 4, 8, 128, 16, 0, F16,
+                                         None) == INV
+    assert lib.orin_kv_cache_write_paged(FAKE, FAKE, 1024, FAKE, FAKE, FAKE, 4, 8, 128, 16, 3,
+                                         F16, None) == INV
+    assert lib.orin_kv_cache_write_paged(FAKE, FAKE, 8 * 36, FAKE, FAKE, FAKE, 4, 8, 36, 16, 0,
+                                         F16, None) == UNS
+    assert lib.orin_kv_cache_convert(FAKE, 1024, FAKE, FAKE, 10, 8, 128, 16, 0, 2, F16,
+                                     None) == INV  # direction
+    assert lib.orin_kv_cache_convert(FAKE, 1024, FAKE, None, 10, 8, 128, 16, 0, 0, F16,
+                                     None) == INV
+    assert lib.orin_rope_sin_cos_cache(FAKE, FAKE, 128, 0, 1e6, None) == INV
+    assert lib.orin_rope_sin_cos_cache(FAKE, FAKE, 128, 64, -1.0, None) == INV
+    # producer: the tokens must fit the cache; head sizes 128 / 256 only
+    assert lib.orin_qk_norm_rope(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0, 64, 60,
+                                 None, 8, 32, 8, 128, 1e-6, F16, None) == INV
+    assert lib.orin_qk_norm_rope(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0, 64, 0,
+                                 None, 8, 32, 8, 64, 1e-6, F16, None) == UNS
+    assert lib.orin_vision_split_rope_transpose(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1024, 16, 71,
+                                                _lib.DTYPE_BF16, None) == INV
+
+
 def test_unsupported_shapes_are_rejected():
     lib = _lib.load()
     assert lib.orin_flash_attention_prefill(0, 16, 4, 4, 100, 1, 0, 64, 400, FAKE, FAKE, FAKE,
