@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-producers", action="store_true",
+                    help="skip the timing of the KV-write / Q-K producer kernels")
     ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 512 MiB device copy (the reference traffic for the "
@@ -101,6 +103,79 @@ def make_decode(dtype, gen, pools, layout=1):
     return dict(B=B, Hq=Hq, Hkv=Hkv, d=d, bs=bs, lens=lens, layout=layout, lens_d=torch.from_numpy(lens).cuda(),
                 bt=torch.from_numpy(bt).cuda(), kp=kp, vp=vp, q=q, o=o, kv_bytes=kv_bytes,
                 maxlen=int(lens.max()))
+
+
+def make_producers(dtype, gen):
+    """Inputs of the kernels either side of the path, at the bench shapes: the Qwen3 Q/K
+    producer for the C3 prefill (4096 tokens, 32 q / 8 kv heads), a paged KV write of
+    the same 4096 tokens (head-major pool, block 16), and the vision QKV split + rotary
+    for C5 (4 x 1024 patches, 16 heads, d 72)."""
+    import torch
+    S, Hq, Hkv, d = 4096, 32, 8, 128
+    dev = "cuda"
+    p = {}
+    p["q"] = torch.randn(S, Hq * d, device=dev, generator=gen).to(dtype)
+    p["k"] = torch.randn(S, Hkv * d, device=dev, generator=gen).to(dtype)
+    p["v"] = torch.randn(S, Hkv * d, device=dev, generator=gen).to(dtype)
+    p["wq"] = torch.ones(d, device=dev, dtype=dtype)
+    p["wk"] = torch.ones(d, device=dev, dtype=dtype)
+    p["sin"] = torch.empty(S, d, device=dev)
+    p["cos"] = torch.empty(S, d, device=dev)
+    p["kc"] = torch.empty(1, S, Hkv * d, device=dev, dtype=dtype)
+    p["vc"] = torch.empty_like(p["kc"])
+    e = torch.tensor([], dtype=dtype).element_size()
+    # q read + written, k and v read, k and v cache rows written, sin/cos tables read
+    p["norm_rope_bytes"] = (2 * S * Hq * d + 4 * S * Hkv * d) * e + 2 * S * d * 4
+    bs = 16
+    nblk = S // bs
+    p["kpool"] = torch.empty(nblk, Hkv, bs, d, device=dev, dtype=dtype)
+    p["vpool"] = torch.empty_like(p["kpool"])
+    perm = torch.randperm(nblk, device=dev, generator=gen).to(torch.int32)
+    t = torch.arange(S, device=dev, dtype=torch.int32)
+    p["slots"] = (perm[t // bs] * bs + t % bs).to(torch.int32)
+    p["scatter_bytes"] = 4 * S * Hkv * d * e  # K and V rows read and written
+    N, H, dv = 4096, 16, 72
+    p["qkv"] = torch.randn(N, 3 * H * dv, device=dev, generator=gen).to(dtype)
+    p["vcos"] = torch.randn(N, dv, device=dev, generator=gen).to(dtype)
+    p["vsin"] = torch.randn(N, dv, device=dev, generator=gen).to(dtype)
+    p["vout"] = [torch.empty(H, N, dv, device=dev, dtype=dtype) for _ in range(3)]
+    p["vision_bytes"] = (2 * N * 3 * H * dv + 2 * N * dv) * e
+    p["shape"] = (S, Hq, Hkv, d, N, H, dv)
+    return p
+
+
+def time_producers(K, p, reps=50):
+    """Mean time (HIP events on the stream the kernels run on) and HBM GB/s of each."""
+    import torch
+    S, Hq, Hkv, d, N, H, dv = p["shape"]
+    K.sin_cos_cache_calc_cu(d, S, p["sin"], p["cos"], 1e6)
+    calls = {
+        "qk_norm_rope_c3": (lambda: K.qk_norm_rope_cu(
+            p["q"], p["k"], p["v"], p["wq"], p["wk"], p["sin"], p["cos"], p["kc"], p["vc"], 0, S,
+            0, S, Hq, Hkv, d), p["norm_rope_bytes"]),
+        "kv_write_paged_4096": (lambda: K.kv_cache_write_paged(
+            p["k"].view(S, Hkv, d), p["v"].view(S, Hkv, d), p["kpool"], p["vpool"], p["slots"],
+            layout=K.KV_LAYOUT_HEAD_MAJOR), p["scatter_bytes"]),
+        "vision_split_rope_c5": (lambda: K.fused_split_rope_transpose_cu(
+            p["qkv"], p["vcos"], p["vsin"], *p["vout"], N, H, dv), p["vision_bytes"]),
+    }
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, (fn, nbytes) in calls.items():
+        for _ in range(5):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def cpu_baseline(pf, dc, min_seconds=8.0):
@@ -240,6 +315,8 @@ def main():
                          "traffic": _bytes(traffic.get("decode_paged_c4"))},
         },
     }
+    if not args.no_producers:
+        out["producers"] = time_producers(K, make_producers(dtype, gen))
     if args.calibration_copy:
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)

@@ -118,10 +118,11 @@ __global__ void __launch_bounds__(kProdThreads) kv_convert_kernel(ConvertArgs a)
 }
 
 // ---------------------------------------------------------------- Q/K norm + RoPE
-// One wave per (token, head) unit: lane j owns the RoPE pairs (j + 64i, j + 64i + d/2).
+// One (token, head) unit per LPU = D / (2 * VEC) lanes: lane l of a unit holds the 16-byte
+// chunk l of each half of the head row, i.e. the RoPE pairs (VEC*l + i, VEC*l + i + D/2).
 // Units 0..Hq-1 of a token are its query heads (rotated in place), units Hq..Hq+Hkv-1
-// its key heads (rotated, written to the K cache) -- each key unit also copies the
-// token's V head row to the V cache.
+// its key heads (rotated, written to the K cache); a key unit also copies the token's V
+// head row to the V cache.
 struct NormRopeArgs {
   void* q;                 // [S, Hq * d], in place
   const void* k;           // [S, Hkv * d]
@@ -138,60 +139,95 @@ struct NormRopeArgs {
   float eps;
 };
 
+template <typename T>
+__device__ __forceinline__ void unpack16(const u32x4& raw, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 x = __builtin_bit_cast(f32x4, raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = x[i];
+  } else {
+    chunk_unpack(Chunk<T>{raw}, out);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack16(const float* x) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  typedef T tv __attribute__((ext_vector_type(VEC)));
+  tv r;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) r[i] = from_f32<T>(x[i]);
+  return __builtin_bit_cast(u32x4, r);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs a) {
-  constexpr int PAIRS = D / 2 / kWave;  // RoPE pairs per lane
-  static_assert(PAIRS >= 1 && D % (2 * kWave) == 0, "head size must be a multiple of 128");
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int LPU = D / 2 / VEC;  // lanes per unit
+  static_assert(LPU >= 1 && LPU <= kWave && (kWave % LPU) == 0, "unsupported head size");
   const int lane = threadIdx.x & 63;
-  const long unit = (long)blockIdx.x * (kProdThreads / kWave) + (threadIdx.x >> 6);
+  const int l = lane % LPU;
+  const long unit = ((long)blockIdx.x * kProdThreads + threadIdx.x) / LPU;
   const int units = a.Hq + a.Hkv;
   const int t = (int)(unit / units);
-  if (t >= a.seq_len) return;
+  const bool live = t < a.seq_len;
   const int u = (int)(unit % units);
   const bool is_q = u < a.Hq;
   const int h = is_q ? u : u - a.Hq;
   const int start = a.pos_ptr ? *a.pos_ptr : a.start_pos;
-  const int pos = start + t;
+  const int pos = start + (live ? t : 0);
 
+  float lo[VEC], hi[VEC];
+  float ss = 0.f;
   const T* x = is_q ? reinterpret_cast<const T*>(a.q) + ((long)t * a.Hq + h) * D
                     : reinterpret_cast<const T*>(a.k) + ((long)t * a.Hkv + h) * D;
-  float lo[PAIRS], hi[PAIRS];
-  float ss = 0.f;
+  if (live) {
+    unpack16<T>(*reinterpret_cast<const u32x4*>(x + VEC * l), lo);
+    unpack16<T>(*reinterpret_cast<const u32x4*>(x + D / 2 + VEC * l), hi);
 #pragma unroll
-  for (int i = 0; i < PAIRS; ++i) {
-    const int j = lane + kWave * i;
-    lo[i] = to_f32(x[j]);
-    hi[i] = to_f32(x[j + D / 2]);
-    ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
+    for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
   }
+  // sum over the unit's LPU lanes (aligned groups; every lane runs the shuffles)
+#pragma unroll
+  for (int m = 1; m < LPU; m <<= 1) ss += shfl_xor_f(ss, m);
+  if (!live) return;
   const T* w = reinterpret_cast<const T*>(is_q ? a.q_weight : a.k_weight);
   if (w) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) ss += shfl_xor_f(ss, m);
     const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    float wl[VEC], wh[VEC];
+    unpack16<T>(*reinterpret_cast<const u32x4*>(w + VEC * l), wl);
+    unpack16<T>(*reinterpret_cast<const u32x4*>(w + D / 2 + VEC * l), wh);
 #pragma unroll
-    for (int i = 0; i < PAIRS; ++i) {
-      const int j = lane + kWave * i;
-      lo[i] = lo[i] * inv * to_f32(w[j]);
-      hi[i] = hi[i] * inv * to_f32(w[j + D / 2]);
+    for (int i = 0; i < VEC; ++i) {
+      lo[i] = lo[i] * inv * wl[i];
+      hi[i] = hi[i] * inv * wh[i];
+    }
+  }
+  // table entries 2j for j = VEC*l .. VEC*l + VEC-1: floats [2 VEC l, 2 VEC l + 2 VEC)
+  const float* sn = a.sin_cache + (long)pos * D + 2 * VEC * l;
+  const float* cs = a.cos_cache + (long)pos * D + 2 * VEC * l;
+  float ro[VEC], rh[VEC];
+#pragma unroll
+  for (int c4 = 0; c4 < VEC / 2; ++c4) {
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + 4 * c4);
+    const f32x4 k4 = *reinterpret_cast<const f32x4*>(cs + 4 * c4);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = 2 * c4 + e;
+      const float sv = s4[2 * e], cv = k4[2 * e];
+      ro[i] = cv * lo[i] - sv * hi[i];
+      rh[i] = cv * hi[i] + sv * lo[i];
     }
   }
   T* out = is_q ? reinterpret_cast<T*>(a.q) + ((long)t * a.Hq + h) * D
                 : reinterpret_cast<T*>(a.k_cache) + (long)pos * a.cache_tok_stride + (long)h * D;
-  const float* sn = a.sin_cache + (long)pos * D;
-  const float* cs = a.cos_cache + (long)pos * D;
-#pragma unroll
-  for (int i = 0; i < PAIRS; ++i) {
-    const int j = lane + kWave * i;
-    const float s = sn[2 * j], c = cs[2 * j];
-    out[j] = from_f32<T>(c * lo[i] - s * hi[i]);
-    out[j + D / 2] = from_f32<T>(c * hi[i] + s * lo[i]);
-  }
+  *reinterpret_cast<u32x4*>(out + VEC * l) = pack16<T>(ro);
+  *reinterpret_cast<u32x4*>(out + D / 2 + VEC * l) = pack16<T>(rh);
   if (!is_q) {
     const T* vr = reinterpret_cast<const T*>(a.v) + ((long)t * a.Hkv + h) * D;
     T* vo = reinterpret_cast<T*>(a.v_cache) + (long)pos * a.cache_tok_stride + (long)h * D;
-#pragma unroll
-    for (int i = 0; i < 2 * PAIRS; ++i) vo[lane + kWave * i] = vr[lane + kWave * i];
+    copy16(vo + VEC * l, vr + VEC * l);
+    copy16(vo + D / 2 + VEC * l, vr + D / 2 + VEC * l);
   }
 }
 
@@ -318,9 +354,10 @@ hipError_t launch_qk_norm_rope(void* q, const void* k, const void* v, const void
                  cache_tok_stride, pos_ptr, start_pos, seq_len, Hq, Hkv, head_size, eps};
   const long units = (long)seq_len * (Hq + Hkv);
   if (units <= 0) return hipSuccess;
-  const unsigned grid = (unsigned)((units + kProdThreads / kWave - 1) / (kProdThreads / kWave));
   return by_dtype(dtype, [&](auto z) {
     using T = decltype(z);
+    const long lpu = head_size / 2 / (16 / (long)sizeof(T));
+    const unsigned grid = grid_for(units * lpu);
     if (head_size == 128)
       hipLaunchKernelGGL((qk_norm_rope_kernel<T, 128>), dim3(grid), dim3(kProdThreads), 0, stream,
                          a);
