@@ -317,6 +317,8 @@ def main():
     }
     if not args.no_producers:
         out["producers"] = time_producers(K, make_producers(dtype, gen))
+        for name, rec in out["producers"].items():
+            rec["traffic"] = _bytes(traffic.get(name))
     if args.calibration_copy:
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
