@@ -20,6 +20,8 @@
 //  vision_qkv_kernel       kernel::fused_split_rope_transpose_cu
 //                          (vision_encoder_kernel.cu:662-773): split [N, 3*H*d] into
 //                          head-major q/k/v [H, N, d] with the 2-D rotary on q and k.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -280,6 +282,70 @@ vision_qkv_kernel(const T* qkv, const T* cos_t, const T* sin_t, T* qo, T* ko, T*
   vo[o + j + half] = row[2 * hidden + j + half];
 }
 
+// Vectorised form for d/2 % 4 == 0 (d = 64, 72, 80, 128 ...): a workgroup owns kVisTok
+// consecutive tokens and every (q|k|v, head) of them; item (which, h, t, c) moves elements
+// [4c, 4c+4) of both halves of one head row.  c runs fastest, then t, so a wave's stores
+// for one head cover kVisTok contiguous output rows and its loads stay inside the
+// workgroup's kVisTok input rows (read from HBM once, reused through L2).
+constexpr int kVisTok = 8;
+
+template <typename T>
+union Chunk4 {
+  typename std::conditional<sizeof(T) == 2, u32x2, u32x4>::type raw;
+  T e[4];
+};
+
+template <typename T>
+__device__ __forceinline__ Chunk4<T> load4(const T* p) {
+  Chunk4<T> c;
+  c.raw = *reinterpret_cast<const decltype(c.raw)*>(p);
+  return c;
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const Chunk4<T>& c) {
+  *reinterpret_cast<decltype(c.raw)*>(p) = c.raw;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kProdThreads)
+vision_qkv4_kernel(const T* qkv, const T* cos_t, const T* sin_t, T* qo, T* ko, T* vo, int N, int H,
+                   int d) {
+  const int half = d / 2, chunks = half / 4;
+  const int t0 = blockIdx.x * kVisTok;
+  const int nt = min(kVisTok, N - t0);
+  const long hidden = (long)H * d;
+  const int per_head = nt * chunks;
+  const int items = 3 * H * per_head;
+  for (int i = threadIdx.x; i < items; i += kProdThreads) {
+    const int wh = i / per_head;  // which * H + h
+    const int r = i - wh * per_head;
+    const int tl = r / chunks, j = (r - tl * chunks) * 4;
+    const int which = wh / H, h = wh - which * H;
+    const int t = t0 + tl;
+    const T* src = qkv + (long)t * 3 * hidden + (long)which * hidden + (long)h * d + j;
+    const long o = ((long)h * N + t) * d + j;
+    T* dst = which == 0 ? qo : which == 1 ? ko : vo;
+    Chunk4<T> x1 = load4(src), x2 = load4(src + half);
+    if (which < 2) {
+      const long tb = (long)t * d + j;
+      const Chunk4<T> c1 = load4(cos_t + tb), s1 = load4(sin_t + tb);
+      const Chunk4<T> c2 = load4(cos_t + tb + half), s2 = load4(sin_t + tb + half);
+      Chunk4<T> y1, y2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = to_f32(x1.e[e]), b = to_f32(x2.e[e]);
+        y1.e[e] = from_f32<T>(__builtin_fmaf(a, to_f32(c1.e[e]), -(b * to_f32(s1.e[e]))));
+        y2.e[e] = from_f32<T>(__builtin_fmaf(a, to_f32(s2.e[e]), b * to_f32(c2.e[e])));
+      }
+      x1 = y1;
+      x2 = y2;
+    }
+    store4(dst + o, x1);
+    store4(dst + o + half, x2);
+  }
+}
+
 unsigned grid_for(long items) { return (unsigned)((items + kProdThreads - 1) / kProdThreads); }
 
 template <typename F>
@@ -384,6 +450,14 @@ hipError_t launch_vision_qkv(const void* qkv, const void* cos_t, const void* sin
     using T = decltype(z);
     const long n = (long)N * H * (d / 2);
     if (n <= 0) return hipSuccess;
+    if ((d / 2) % 4 == 0) {
+      hipLaunchKernelGGL(vision_qkv4_kernel<T>, dim3((N + kVisTok - 1) / kVisTok),
+                         dim3(kProdThreads), 0, stream, reinterpret_cast<const T*>(qkv),
+                         reinterpret_cast<const T*>(cos_t), reinterpret_cast<const T*>(sin_t),
+                         reinterpret_cast<T*>(q), reinterpret_cast<T*>(k),
+                         reinterpret_cast<T*>(v), N, H, d);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(vision_qkv_kernel<T>, dim3(grid_for(n)), dim3(kProdThreads), 0, stream,
                        reinterpret_cast<const T*>(qkv), reinterpret_cast<const T*>(cos_t),
                        reinterpret_cast<const T*>(sin_t), reinterpret_cast<T*>(q),

@@ -236,3 +236,47 @@ def test_c4_paged_decode_full_size(kind, layout):
     torch.cuda.synchronize()
     ref = oracle.decode_paged(q, kp, vp, bt, lens, nthreads=8)
     assert_lowp_close(host(o), ref, what="C4 paged decode")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+def test_gpu_pos_decode_graph_replay(kind):
+    """orin_flash_attention_decode_gpu_pos captured once in a HIP graph and replayed with
+    the position (and query) changed on the device between replays: every replay equals
+    the eager call bit for bit and the oracle within the 16-bit bar."""
+    rng = np.random.default_rng(21)
+    head_num, kv_heads, d, max_seq, layers, layer = 32, 8, 128, 4096, 2, 1
+    kv_dim, kv_mul = kv_heads * d, head_num // kv_heads
+    kc = quantize(normal(rng, (layers, max_seq, kv_dim)), kind)
+    vc = quantize(normal(rng, (layers, max_seq, kv_dim)), kind)
+    kd, vd = dev(kc, kind), dev(vc, kind)
+    qd = torch.zeros(head_num * d, device="cuda", dtype=TORCH[kind])
+    p = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.zeros(head_num * d, device="cuda", dtype=TORCH[kind])
+    K.reserve_decode_workspace(head_num, d, max_seq)
+
+    def call(o):
+        K.flash_attention_decode_fp16_gpu_pos_cu(p, head_num, kv_heads, d, kv_mul, layer,
+                                                 max_seq, kv_dim, qd, o, kd, vd)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(out)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(out)
+    for pos in [4095, 5, 1000, 0, 2047]:
+        q = quantize(normal(rng, head_num * d), kind)
+        qd.copy_(dev(q, kind))
+        p.fill_(pos)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager = torch.zeros_like(out)
+        call(eager)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay at pos {pos} differs from eager"
+        ref, _ = oracle.mha_kernel(pos, head_num, layer, max_seq, kv_dim, kv_mul, d, q, kc, vc)
+        assert_lowp_close(host(out), ref, what=f"{kind} graph replay pos {pos}")

@@ -242,13 +242,16 @@ def test_producer_then_prefill_matches_oracle():
 # ---------------------------------------------------------------- vision producer
 
 @pytest.mark.parametrize("kind", KINDS)
-def test_vision_split_rope_transpose(kind):
-    """qkv [N, 3*H*d] -> q/k/v [H, N, d] with the 2-D rotary of a 32x32 grid on q and k."""
-    rng = np.random.default_rng(5)
-    H, d, grid = 16, 72, 32
-    N = grid * grid
+@pytest.mark.parametrize("d,gh,gw", [(72, 32, 32), (72, 26, 22), (80, 26, 22), (76, 26, 22)])
+def test_vision_split_rope_transpose(kind, d, gh, gw):
+    """qkv [N, 3*H*d] -> q/k/v [H, N, d] with the 2-D rotary of a gh x gw grid on q and k.
+    d/2 % 4 == 0 takes the 8-token vectorised kernel (572 tokens leaves a ragged last
+    workgroup); d = 76 takes the per-pair kernel."""
+    rng = np.random.default_rng(5 + d + gh)
+    H = 16
+    N = gh * gw
     qkv = normal(rng, (N, 3 * H * d))
-    c, s = oracle.vision_cos_sin(1, grid, grid, 2, d)
+    c, s = oracle.vision_cos_sin(1, gh, gw, 2, d)
     out = [torch.empty(H, N, d, dtype=TORCH[kind], device="cuda") for _ in range(3)]
     K.fused_split_rope_transpose_cu(dev(qkv, kind), dev(c, kind), dev(s, kind), *out, N, H, d)
     torch.cuda.synchronize()
