@@ -431,8 +431,9 @@ decode_split_kernel(DecodeArgs a) {
 }
 
 // Merge split partials of every (row, head) whose row needed more than one split.
-// One wave per (row, head): lanes read the splits' (m, l) in parallel, the weights
-// exp2(m_s - M) / L go through LDS, then every lane forms D/64 outputs.
+// One wave per (row, head): the splits' (m, l) are staged in LDS by the lanes in
+// parallel, then lane l forms outputs [l * D/64, (l + 1) * D/64) with the acc loads of
+// eight splits in flight at a time.
 template <typename T, int D>
 __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   constexpr int EPL = D / kWave;
@@ -441,34 +442,47 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   const int len = row_len(a, row);
   const int nsplit = len > 0 ? (len + a.split_tokens - 1) / a.split_tokens : 0;
   if (nsplit <= 1) return;
-  const int lane = threadIdx.x;
-  const float* p = a.ws + ((long)row * a.Hq + h) * a.max_splits * (D + 2);
-  __shared__ float s_w[kMaxCombineSplits];
+  const float* ph = a.ws + ((long)row * a.Hq + h) * a.max_splits * (D + 2);
+  __shared__ float s_m[kMaxCombineSplits], s_l[kMaxCombineSplits];
   float M = -INFINITY;
-  for (int s = lane; s < nsplit; s += kWave) M = fmaxf(M, p[s * (D + 2) + D]);
+  for (int sp = threadIdx.x; sp < nsplit; sp += kWave) {
+    const float m = ph[sp * (D + 2) + D];
+    s_m[sp] = m;
+    s_l[sp] = ph[sp * (D + 2) + D + 1];
+    M = fmaxf(M, m);
+  }
 #pragma unroll
   for (int mask = 32; mask >= 1; mask >>= 1) M = fmaxf(M, shfl_xor_f(M, mask));
-  float L = 0.f;
-  for (int s = lane; s < nsplit; s += kWave) {
-    const float w = fast_exp2(p[s * (D + 2) + D] - M);
-    s_w[s] = w;
-    L += w * p[s * (D + 2) + D + 1];
-  }
-#pragma unroll
-  for (int mask = 32; mask >= 1; mask >>= 1) L += shfl_xor_f(L, mask);
   __syncthreads();
-  const float inv = 1.f / L;
-  float o[EPL];
+  float L = 0.f, o[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) o[e] = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float w = s_w[s];
+  const float* pl = ph + threadIdx.x * EPL;
+  int sp = 0;
+  for (; sp + 8 <= nsplit; sp += 8) {
+    float x[8][EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) o[e] = __builtin_fmaf(w, p[s * (D + 2) + lane * EPL + e], o[e]);
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[u][e] = pl[(sp + u) * (D + 2) + e];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float f = fast_exp2(s_m[sp + u] - M);
+      L = __builtin_fmaf(f, s_l[sp + u], L);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = __builtin_fmaf(f, x[u][e], o[e]);
+    }
   }
+  for (; sp < nsplit; ++sp) {
+    const float f = fast_exp2(s_m[sp] - M);
+    L = __builtin_fmaf(f, s_l[sp], L);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = __builtin_fmaf(f, pl[sp * (D + 2) + e], o[e]);
+  }
+  const float inv = 1.f / L;
   T* out = reinterpret_cast<T*>(a.o) + (long)row * a.o_row_stride + (long)h * a.o_head_stride;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) out[lane * EPL + e] = from_f32<T>(o[e] * inv);
+  for (int e = 0; e < EPL; ++e) out[threadIdx.x * EPL + e] = from_f32<T>(o[e] * inv);
 }
 
 template <typename T, int D, int G>

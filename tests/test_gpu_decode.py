@@ -200,6 +200,40 @@ def test_split_count_invariance():
         assert_fp32_close(o, outs[0], d, what="split invariance")
 
 
+def test_split_merge_repeatable_across_streams():
+    """Split partials and their merge: repeated launches, on one stream and on two
+    streams running at once (separate outputs, shared inputs), give the first launch's
+    output bit for bit."""
+    rng = np.random.default_rng(14)
+    B, Hq, Hkv, d = 5, 32, 8, 128
+    lens = np.array([1, 100, 700, 2000, 4000], np.int32)
+    kc = quantize(normal(rng, (B, 4000, Hkv, d)), "fp16")
+    vc = quantize(normal(rng, (B, 4000, Hkv, d)), "fp16")
+    q = quantize(normal(rng, (B, Hq, d)), "fp16")
+    qd, kd, vd = dev(q, "fp16"), dev(kc, "fp16"), dev(vc, "fp16")
+    lens_d = torch.from_numpy(lens).cuda()
+
+    def call(o):
+        K.batched_decode_cu(qd, kd, vd, o, lens_d, 4000, Hkv, split_tokens=256)
+
+    first = torch.zeros(B, Hq, d, device="cuda", dtype=torch.float16)
+    call(first)
+    torch.cuda.synchronize()
+    ref = oracle.decode_contig(q, kc, vc, lens)
+    assert_lowp_close(host(first), ref, what="split merge")
+    outs = [torch.zeros_like(first) for _ in range(7)]
+    for o in outs[:3]:
+        call(o)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for i in range(2):
+        for j, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                call(outs[3 + 2 * i + j])
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, first), f"launch {i} differs"
+
+
 def test_zero_length_rows_give_zeros():
     rng = np.random.default_rng(13)
     B, Hq, Hkv, d = 3, 8, 8, 64
