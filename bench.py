@@ -213,6 +213,18 @@ def cpu_baseline(pf, dc, min_seconds=8.0):
         dreps += 1
     t_dc = (time.perf_counter() - t0) / dreps
     kv_bytes = 2 * int(lens.sum()) * Hkv * d * 2
+
+    # One core, as the reference's CPU path runs: every 8th query row of the C3 prefill
+    # and the first 4 C4 sequences.
+    rows = np.arange(0, S, 8)
+    t0 = time.perf_counter()
+    oracle.prefill_causal(0, q, k, v, Hq, Hkv, d, rows=rows, nthreads=1)
+    t1_pf = time.perf_counter() - t0
+    flops1 = float(np.sum(4.0 * d * Hq * (rows + 1)))
+    t0 = time.perf_counter()
+    oracle.decode_paged(qd[:4], kp, vp, bt[:4], lens[:4], nthreads=1)
+    t1_dc = time.perf_counter() - t0
+    bytes1 = 2 * int(lens[:4].sum()) * Hkv * d * 2
     return {
         "value": flops / t_pf / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
         "sample": f"the full C3 causal prefill ({S} rows x {Hq} heads), fp32 oracle on "
@@ -220,6 +232,11 @@ def cpu_baseline(pf, dc, min_seconds=8.0):
         "decode": {"value": kv_bytes / t_dc / 1e9, "unit": "GB/s",
                    "sample": f"the full C4 paged decode ({nseq} sequences), {dreps} runs, "
                              f"{t_dc * 1e3:.1f} ms each"},
+        "single_thread": {
+            "prefill_TFLOP/s": flops1 / t1_pf / 1e12, "decode_GB/s": bytes1 / t1_dc / 1e9,
+            "cores": 1,
+            "sample": f"{len(rows)} query rows (every 8th) of C3 in {t1_pf:.1f} s; 4 of the C4 "
+                      f"sequences in {t1_dc * 1e3:.0f} ms"},
     }
 
 

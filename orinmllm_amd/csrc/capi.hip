@@ -33,11 +33,12 @@ int round_up(long x, int m) { return (int)((x + m - 1) / m * m); }
 constexpr int kMaxSplits = 1024;
 
 // Tokens per split for a decode launch with `base_blocks` (row, kv head, head group)
-// units and rows of up to max_len tokens.  Aims at ~4096 workgroups (16 per CU) with
-// at least 256 tokens (one 64-token tile per wave) per split.
+// units and rows of up to max_len tokens.  Aims at ~3328 workgroups (13 per CU, i.e.
+// about 3.25 rounds of the 4 resident per CU; measured best on the batch-32 paged
+// decode) with at least 256 tokens (one 64-token tile per wave) per split.
 int auto_split_tokens(long base_blocks, int max_len) {
   if (max_len <= 0) return 256;
-  const long target = 4096;
+  const long target = 3328;
   long splits = (target + base_blocks - 1) / base_blocks;
   if (splits < 1) splits = 1;
   int st = round_up((max_len + splits - 1) / splits, 64);

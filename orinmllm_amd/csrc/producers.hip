@@ -76,16 +76,19 @@ __global__ void __launch_bounds__(kProdThreads) kv_scatter_kernel(ScatterArgs a)
   const int r = (int)(idx / chunks_per_row);
   if (r >= a.n_rows) return;
   const int c = (int)(idx % chunks_per_row);
+  const int h = c / chunks_per_head, e = (c % chunks_per_head) * VEC;
+  // The source rows do not depend on the slot: their loads go out with the slot's.
+  const long src = (long)r * a.src_row_stride + (long)h * a.head_size + e;
+  const u32x4 kx = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.k_src) + src);
+  const u32x4 vx = *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.v_src) + src);
   const int slot = a.slots[r];
   if (slot < 0) return;
-  const int h = c / chunks_per_head, e = (c % chunks_per_head) * VEC;
   const long blk = slot / a.block_size, off = slot % a.block_size;
   const long dst = a.head_major
                        ? ((blk * a.kv_heads + h) * a.block_size + off) * a.head_size + e
                        : ((blk * a.block_size + off) * a.kv_heads + h) * a.head_size + e;
-  const long src = (long)r * a.src_row_stride + (long)h * a.head_size + e;
-  copy16(reinterpret_cast<T*>(a.k_pool) + dst, reinterpret_cast<const T*>(a.k_src) + src);
-  copy16(reinterpret_cast<T*>(a.v_pool) + dst, reinterpret_cast<const T*>(a.v_src) + src);
+  *reinterpret_cast<u32x4*>(reinterpret_cast<T*>(a.k_pool) + dst) = kx;
+  *reinterpret_cast<u32x4*>(reinterpret_cast<T*>(a.v_pool) + dst) = vx;
 }
 
 // ---------------------------------------------------------------- contiguous <-> paged
