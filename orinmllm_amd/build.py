@@ -19,6 +19,10 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborin_attn.so")
 SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "capi.hip"]
+# C++ host mirror of kuiper's kernel:: functions and op:: layers over the C ABI.
+HOST_DIR = os.path.join(PKG_DIR, "cpp")
+HOST_SOURCES = ["base.cpp", "kernels.cpp", "layers.cpp"]
+HOST_LIB_PATH = os.path.join(PKG_DIR, "liborin_attn_host.so")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -50,8 +54,32 @@ def _compile(src: str) -> str:
     return obj
 
 
+def build_host(verbose: bool = False) -> str:
+    """Compile the C++ host mirror into liborin_attn_host.so, linked to liborin_attn.so."""
+    objs = []
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD_DIR, "host_" + os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), "-std=c++17", "-O2", "-fPIC", "-Wall", "-I", os.path.join(HOST_DIR, "include"),
+               "-I", os.path.join(REPO, "include"), "-c", os.path.join(HOST_DIR, "src", src), "-o", obj]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+        objs.append(obj)
+    tmp = HOST_LIB_PATH + ".tmp"
+    cmd = [hipcc(), "-shared", "-fPIC", "-o", tmp, *objs, "-L", PKG_DIR, "-lorin_attn",
+           "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host link failed:\n{res.stderr}")
+    os.replace(tmp, HOST_LIB_PATH)
+    if verbose:
+        print(f"built {HOST_LIB_PATH}")
+    return HOST_LIB_PATH
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> str:
-    """Compile every HIP source for gfx950 and link liborin_attn.so. Always recompiles."""
+    """Compile every HIP source for gfx950 and link liborin_attn.so, then the C++ host
+    mirror liborin_attn_host.so. Always recompiles."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -64,6 +92,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_host(verbose)
     return LIB_PATH
 
 
