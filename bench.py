@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-producers", action="store_true",
                     help="skip the timing of the KV-write / Q-K producer kernels")
     ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
+    ap.add_argument("--no-decode-4096", action="store_true",
+                    help="skip the decode with every KV length 4096")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 512 MiB device copy (the reference traffic for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -79,12 +81,15 @@ def make_prefill(dtype, gen):
     return dict(S=S, Hq=Hq, Hkv=Hkv, d=d, q=q, k=k, v=v, o=o, flops=flops)
 
 
-def make_decode(dtype, gen, pools, layout=1):
+def make_decode(dtype, gen, pools, layout=1, uniform_len=None):
+    """C4 inputs: KV lengths U[512, 4096] (seeded), or all equal to uniform_len."""
     import numpy as np
     import torch
     B, Hq, Hkv, d, bs = 32, 32, 8, 128, 16
     rng = np.random.default_rng(0xC4)
     lens = rng.integers(512, 4097, B).astype(np.int32)
+    if uniform_len is not None:
+        lens = np.full(B, uniform_len, np.int32)
     nblk = (lens + bs - 1) // bs
     total = int(nblk.sum())
     maxb = int(nblk.max())
@@ -103,6 +108,42 @@ def make_decode(dtype, gen, pools, layout=1):
     return dict(B=B, Hq=Hq, Hkv=Hkv, d=d, bs=bs, lens=lens, layout=layout, lens_d=torch.from_numpy(lens).cuda(),
                 bt=torch.from_numpy(bt).cuda(), kp=kp, vp=vp, q=q, o=o, kv_bytes=kv_bytes,
                 maxlen=int(lens.max()))
+
+
+def time_decode_uniform(K, dtype, gen, pools, reps=50):
+    """The batch-32 paged decode with every KV length 4096 (the length the decode target
+    is stated at), timed like the C4 decode: automatic split size, and 1024-token splits
+    passed explicitly (split_tokens is part of the API for callers that know their
+    lengths)."""
+    import torch
+    dc = make_decode(dtype, gen, pools, uniform_len=4096)
+    stream = torch.cuda.current_stream()
+    out = {"kv_bytes_per_call": dc["kv_bytes"]}
+    for name, st in [("auto_split", 0), ("split_1024", 1024)]:
+        nb = K.decode_workspace_size(dc["B"], dc["Hq"], dc["Hkv"], dc["d"], dc["maxlen"], st)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+
+        def run(i):
+            p = i % pools
+            K.paged_decode_cu(dc["q"], dc["kp"][p], dc["vp"][p], dc["o"], dc["bt"],
+                              dc["lens_d"], dc["maxlen"], split_tokens=st, workspace=ws,
+                              layout=dc["layout"])
+
+        for i in range(10):
+            run(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            run(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = dc["kv_bytes"] / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    del dc
+    torch.cuda.empty_cache()
+    return out
 
 
 def make_producers(dtype, gen):
@@ -332,6 +373,8 @@ def main():
                          "traffic": _bytes(traffic.get("decode_paged_c4"))},
         },
     }
+    if not args.no_decode_4096:
+        out["decode_kv4096"] = time_decode_uniform(K, dtype, gen, args.pools)
     if not args.no_producers:
         out["producers"] = time_producers(K, make_producers(dtype, gen))
         for name, rec in out["producers"].items():
