@@ -35,7 +35,7 @@ namespace orin {
 
 namespace {
 
-constexpr int PD = 128;            // head size
+constexpr int PD = 128;            // largest head size; K/V rows occupy PD elements in LDS
 constexpr int PBN = 64;            // keys per tile
 constexpr int PNW = 8;             // waves per workgroup
 constexpr int PBM = 32 * PNW;      // query rows per workgroup
@@ -135,8 +135,29 @@ __device__ __forceinline__ u32x2 lds_read_tr(lds_ptr p, int byte_off) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-template <typename T, bool CAUSAL>
+// Order of the MFMAs of one phase: QK steps (2 per 16-wide slice of the head) and PV steps
+// (DT per 16-key chunk) alternate while both remain, so that consecutive MFMAs on one
+// accumulator are at least two apart.
+template <int NQK, int NPV>
+struct PhaseOrder {
+  int is_qk[NQK + NPV];
+  int idx[NQK + NPV];
+  constexpr PhaseOrder() : is_qk(), idx() {
+    int q = 0, v = 0;
+    for (int i = 0; i < NQK + NPV; ++i) {
+      const bool take_qk = q < NQK && (v >= NPV || i % 2 == 0);
+      is_qk[i] = take_qk;
+      idx[i] = take_qk ? q++ : v++;
+    }
+  }
+};
+
+template <typename T, bool CAUSAL, int D>
 __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
+  static_assert(D % 8 == 0 && D <= PD, "head size: a multiple of 8 up to 128");
+  constexpr int QS = (D + 15) / 16;  // 16-wide slices of the QK contraction (zero-padded)
+  constexpr int DT = (D + 31) / 32;  // 32-wide output tiles of O^T
+  constexpr int NCH = D / 8;         // valid 16-byte chunks of a K / V row
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -203,8 +224,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     const int row = 4 * (2 * wave + i) + (lane >> 4);
     const int pc = lane & 15;
     k_row[i] = row;
-    k_col[i] = 8 * (pc ^ (row & 15));
-    v_col[i] = 8 * (pc ^ (4 * (row & 3)));
+    // Chunks past the row (head sizes below 128) load chunk 0 of the same row instead:
+    // finite values that meet zero Q elements (K) or fill O^T rows never stored (V).
+    const int kc = pc ^ (row & 15), vc = pc ^ (4 * (row & 3));
+    k_col[i] = 8 * (kc < NCH ? kc : 0);
+    v_col[i] = 8 * (vc < NCH ? vc : 0);
   }
   char* const k_lds = smem;
   char* const v_lds = smem + PKREGION;
@@ -248,14 +272,14 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 
   // ------------------------------------------------------------ Q fragments
-  u32x4 qf[8];
+  u32x4 qf[QS];
   {
     const T* qp = reinterpret_cast<const T*>(a.q) + (long)(seg_start + qi) * a.q_tok_stride +
                   (long)head * a.q_head_stride;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (qi < q_n) val = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * hf);
+    for (int s = 0; s < QS; ++s) {
+      u32x4 val = {0u, 0u, 0u, 0u};  // rows past the end and the zero padding of the head
+      if (qi < q_n && 16 * s + 8 * hf < D) val = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * hf);
       qf[s] = val;
     }
   }
@@ -268,9 +292,9 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   else wait_vmcnt<4>();
   step_barrier();
 
-  f32x16 oacc[4];
+  f32x16 oacc[DT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
   f32x16 sacc[2];
@@ -298,12 +322,13 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+    constexpr int NQK = 2 * QS;
     u32x4 fr[PF + 1];
 #pragma unroll
     for (int i = 0; i < PF; ++i) fr[i] = k_frag(0, i & 1, i >> 1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + PF < 16) fr[(i + PF) % (PF + 1)] = k_frag(0, (i + PF) & 1, (i + PF) >> 1);
+    for (int i = 0; i < NQK; ++i) {
+      if (i + PF < NQK) fr[(i + PF) % (PF + 1)] = k_frag(0, (i + PF) & 1, (i + PF) >> 1);
       sacc[i & 1] = mfma32<T>(fr[i % (PF + 1)], qf[i >> 1], sacc[i & 1]);
     }
   };
@@ -314,7 +339,9 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // read from LDS three MFMAs before its use.
   auto mphase = [&](auto slot_tag, auto qk_tag) __attribute__((always_inline)) {
     constexpr bool QK = decltype(qk_tag)::value;
-    constexpr int N = QK ? 32 : 16;
+    constexpr int NQK = QK ? 2 * QS : 0, NPV = 4 * DT;
+    constexpr int N = NQK + NPV;
+    constexpr PhaseOrder<NQK, NPV> order{};
     constexpr int sl_off = decltype(slot_tag)::value * PTILE_BYTES;
     if (QK) {
 #pragma unroll
@@ -322,11 +349,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
     }
-    // MFMA i: QK step i/2 (even i) or PV step i/2 (odd i) when QK; PV step i otherwise.
+    // MFMA i: QK step j = (kt = j & 1, slice j >> 1) or PV step n = (chunk n / DT, d-tile
+    // n % DT), in the order of PhaseOrder.
     auto fetch = [&](int i) __attribute__((always_inline)) {
-      if (QK && !(i & 1)) return k_frag(sl_off, (i >> 1) & 1, i >> 2);
-      const int n = QK ? (i >> 1) : i;
-      return v_frag(sl_off, n >> 2, n & 3);
+      if (order.is_qk[i]) return k_frag(sl_off, order.idx[i] & 1, order.idx[i] >> 1);
+      return v_frag(sl_off, order.idx[i] / DT, order.idx[i] % DT);
     };
     u32x4 fr[PF + 1];
 #pragma unroll
@@ -334,12 +361,12 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       if (i + PF < N) fr[(i + PF) % (PF + 1)] = fetch(i + PF);
-      if (QK && !(i & 1)) {
-        const int j = i >> 1;  // QK step: kt = j & 1, s = j >> 1
+      if (order.is_qk[i]) {
+        const int j = order.idx[i];
         sacc[j & 1] = mfma32<T>(fr[i % (PF + 1)], qf[j >> 1], sacc[j & 1]);
       } else {
-        const int n = QK ? (i >> 1) : i;
-        oacc[n & 3] = mfma32<T>(fr[i % (PF + 1)], pf[n >> 2], oacc[n & 3]);
+        const int n = order.idx[i];
+        oacc[n % DT] = mfma32<T>(fr[i % (PF + 1)], pf[n / DT], oacc[n % DT]);
       }
     }
   };
@@ -373,7 +400,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       const float alpha = fast_exp2(m_old - m_new);
       l_run *= alpha;
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
+      for (int d = 0; d < DT; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
     }
@@ -473,10 +500,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
             (long)head * a.o_head_stride;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < DT; ++t)
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
         const int d0 = t * 32 + 8 * rg + 4 * hf;
+        if (d0 >= D) continue;  // padding columns of O^T
         u32x2 pk = {pack2<T>(oacc[t][4 * rg] * inv, oacc[t][4 * rg + 1] * inv),
                     pack2<T>(oacc[t][4 * rg + 2] * inv, oacc[t][4 * rg + 3] * inv)};
         *reinterpret_cast<u32x2*>(op + d0) = pk;
@@ -484,8 +512,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 }
 
-template <typename T, bool CAUSAL>
-hipError_t launch_pp_t(const FwdArgs& a, hipStream_t stream) {
+template <typename T, bool CAUSAL, int D>
+hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
   long blocks;
   if (CAUSAL) blocks = (long)((a.n_q + PBM - 1) / PBM) * a.Hq;
   else blocks = (long)a.n_seg * ((a.max_seqlen + PBM - 1) / PBM) * a.Hq;
@@ -495,20 +523,34 @@ hipError_t launch_pp_t(const FwdArgs& a, hipStream_t stream) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev >= 64 || !(__atomic_load_n(&configured, __ATOMIC_ACQUIRE) & (1ull << dev))) {
-    e = hipFuncSetAttribute((const void*)fwd_pp_kernel<T, CAUSAL>,
+    e = hipFuncSetAttribute((const void*)fwd_pp_kernel<T, CAUSAL, D>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, PLDS_BYTES);
     if (e != hipSuccess) return e;
     if (dev < 64) __atomic_fetch_or(&configured, 1ull << dev, __ATOMIC_RELEASE);
   }
-  hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL>), dim3((unsigned)blocks), dim3(PTHREADS),
+  hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D>), dim3((unsigned)blocks), dim3(PTHREADS),
                      PLDS_BYTES, stream, a);
   return hipGetLastError();
+}
+
+template <typename T, bool CAUSAL>
+hipError_t launch_pp_t(const FwdArgs& a, hipStream_t stream) {
+  switch (a.head_size) {
+    case 64: return launch_pp_d<T, CAUSAL, 64>(a, stream);
+    case 72: return launch_pp_d<T, CAUSAL, 72>(a, stream);
+    case 80: return launch_pp_d<T, CAUSAL, 80>(a, stream);
+    case 96: return launch_pp_d<T, CAUSAL, 96>(a, stream);
+    case 128: return launch_pp_d<T, CAUSAL, 128>(a, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 bool fwd_pp_supports(const FwdArgs& a, int dtype) {
-  if (a.head_size != PD || !(dtype == kF16 || dtype == kBF16)) return false;
+  const int d = a.head_size;
+  if (!(d == 64 || d == 72 || d == 80 || d == 96 || d == 128) || !(dtype == kF16 || dtype == kBF16))
+    return false;
   // K/V rows and Q/O rows are read as 16-byte chunks.
   return a.kv_tok_stride % 8 == 0 && a.kv_head_stride % 8 == 0 && a.q_tok_stride % 8 == 0 &&
          a.q_head_stride % 8 == 0;

@@ -37,10 +37,12 @@ def test_pp_output_aliases_query():
 
 
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
-def test_pp_varlen_bidirectional(kind):
-    """4 segments (one ragged) x 16 heads, d 128: 256 workgroups of 256 queries."""
-    rng = np.random.default_rng(11)
-    H, d = 16, 128
+@pytest.mark.parametrize("d", [128, 96, 80, 72, 64])
+def test_pp_varlen_bidirectional(kind, d):
+    """4 segments (one ragged) x 16 heads: 256 workgroups of 256 queries.  Head sizes
+    below 128 pad the QK contraction to a multiple of 16 and O^T to a multiple of 32."""
+    rng = np.random.default_rng(11 + d)
+    H = 16
     cu = np.array([0, 1024, 2048, 2900, 3924], np.int32)
     q, k, v = vision_inputs(rng, cu, H, d, kind)
     N = int(cu[-1])
@@ -52,3 +54,16 @@ def test_pp_varlen_bidirectional(kind):
                                      rng.integers(0, N, 48)]))
     ref = oracle.varlen_bidir(q, k, v, cu, rows=rows, nthreads=8)
     assert_lowp_close(out.float().cpu().numpy()[rows], ref, what=f"pp varlen {kind}")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("d", [64, 96])
+def test_pp_causal_small_head(kind, d):
+    """Causal GQA prefill with head sizes below 128 on the ping-pong kernel (S 2048 x 32
+    heads = 256 workgroups)."""
+    rng = np.random.default_rng(d)
+    S, Hq, Hkv = 2048, 32, 8
+    q, kc, vc, out = run_prefill(kind, 0, S, Hq, Hkv, d, S, 1, 0, rng)
+    rows = sample_rows(S, 40, rng)
+    ref = oracle.prefill_causal(0, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
+    assert_lowp_close(out[rows], ref, what=f"pp causal d {d} {kind}")
