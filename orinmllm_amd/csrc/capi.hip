@@ -95,6 +95,19 @@ int library_workspace(size_t bytes, void** out) {
   return ORIN_OK;
 }
 
+// Compute units of the current device (cached per process; 256 if the query fails).
+int device_cus() {
+  static const int cached = [] {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    return cus;
+  }();
+  return cached;
+}
+
 DecodeArgs decode_defaults() {
   DecodeArgs a = {};
   a.max_splits = 1;
@@ -298,6 +311,16 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
   a.kv_mul = kv_mul;
   a.head_size = head_size;
   a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  // Too few query blocks to fill the device: split their keys (library workspace).
+  size_t split_bytes = 0;
+  const int chunk = fwd_pp_key_split(a, dtype, device_cus(), &split_bytes);
+  if (chunk > 0) {
+    void* ws = nullptr;
+    const int st = library_workspace(split_bytes, &ws);
+    if (st != ORIN_OK) return st;
+    a.key_chunk_tiles = chunk;
+    a.ws = static_cast<float*>(ws);
+  }
   return hip_status(launch_fwd_causal(a, dtype, (hipStream_t)stream));
 }
 

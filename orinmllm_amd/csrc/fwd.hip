@@ -469,8 +469,9 @@ hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
-// Head size 128 goes to the ping-pong kernel (256-query workgroups, one per CU) when its
-// grid covers every CU at least once.  ORIN_FWD_KERNEL=tile|pp overrides the choice (for
+// Head sizes 64-128 go to the ping-pong kernel (256-query workgroups, one per CU) when its
+// grid covers every CU at least once, or when the caller planned a key split for a causal
+// launch that does not (fwd_pp_key_split).  ORIN_FWD_KERNEL=tile|pp overrides the choice (for
 // measurements and tests); unset or any other value keeps it.
 template <bool CAUSAL>
 bool use_pp(const FwdArgs& a, int dtype) {
@@ -482,7 +483,7 @@ bool use_pp(const FwdArgs& a, int dtype) {
     return -1;
   }();
   if (mode == 0 || !fwd_pp_supports(a, dtype)) return false;
-  if (mode == 1) return true;
+  if (mode == 1 || (CAUSAL && a.key_chunk_tiles > 0)) return true;
   const long blocks = CAUSAL ? (long)((a.n_q + 255) / 256) * a.Hq
                              : (long)a.n_seg * ((a.max_seqlen + 255) / 256) * a.Hq;
   return blocks >= 256;

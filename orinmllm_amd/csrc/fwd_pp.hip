@@ -135,6 +135,47 @@ __device__ __forceinline__ u32x2 lds_read_tr(lds_ptr p, int byte_off) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// Key split of causal query block qb (rows qb*PBM ..): `diag` = the first tile holding a
+// key past the block's first query position; tiles [0, diag) are cut into chunks of C
+// tiles and tiles [diag, tiles) join the last chunk, so every chunk shows each of the
+// block's queries at least one key.
+__host__ __device__ inline int pp_block_tiles(const FwdArgs& a, int qb) {
+  return (a.start_pos + min((qb + 1) * PBM, a.n_q) + PBN - 1) / PBN;
+}
+__host__ __device__ inline int pp_block_diag(const FwdArgs& a, int qb) {
+  return (a.start_pos + qb * PBM) / PBN;
+}
+__host__ __device__ inline int pp_block_chunks(const FwdArgs& a, int qb, int C) {
+  const int diag = pp_block_diag(a, qb);
+  return diag > 0 ? (diag + C - 1) / C : 1;
+}
+// Work item `item` of a key-split launch, query blocks last to first: block qb, chunk c.
+__host__ __device__ inline void pp_item(const FwdArgs& a, int item, int C, int* qb, int* c) {
+  const int nqb = (a.n_q + PBM - 1) / PBM;
+  for (int b = nqb - 1; b >= 0; --b) {
+    const int n = pp_block_chunks(a, b, C);
+    if (item < n) {
+      *qb = b;
+      *c = item;
+      return;
+    }
+    item -= n;
+  }
+  *qb = -1;
+  *c = 0;
+}
+__host__ __device__ inline int pp_items(const FwdArgs& a, int C) {
+  const int nqb = (a.n_q + PBM - 1) / PBM;
+  int n = 0;
+  for (int b = 0; b < nqb; ++b) n += pp_block_chunks(a, b, C);
+  return n;
+}
+// Workspace of a key split: O rows [items * Hq * PBM][head_size] in the 16-bit input
+// type, then (m, l) [items * Hq * PBM][2] fp32.  Offsets in floats.
+__host__ __device__ inline long pp_ml_offset(const FwdArgs& a, int D) {
+  return (long)pp_items(a, a.key_chunk_tiles) * a.Hq * PBM * D / 2;
+}
+
 // Order of the MFMAs of one phase: QK steps (2 per 16-wide slice of the head) and PV steps
 // (DT per 16-key chunk) alternate while both remain, so that consecutive MFMAs on one
 // accumulator are at least two apart.
@@ -170,7 +211,23 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 
   // ------------------------------------------------------------ block -> (head, rows)
   int head, q_lo, q_n, seg_start, kv_end, pos_off;
-  if (CAUSAL) {
+  int t_lo = 0, t_hi_split = 0;  // key split: this workgroup's tiles [t_lo, t_hi_split)
+  bool partial = false;          // key split: write fp32 partials, merged by a second launch
+  const int C = a.key_chunk_tiles;
+  if (CAUSAL && C > 0) {
+    head = (int)blockIdx.x % a.Hq;
+    int qb, c;
+    pp_item(a, (int)blockIdx.x / a.Hq, C, &qb, &c);
+    const int n_ch = pp_block_chunks(a, qb, C);
+    t_lo = c * C;
+    t_hi_split = c + 1 < n_ch ? (c + 1) * C : pp_block_tiles(a, qb);
+    partial = n_ch > 1;
+    q_lo = qb * PBM;
+    q_n = a.n_q;
+    seg_start = 0;
+    pos_off = a.start_pos;
+    kv_end = a.start_pos + min(q_lo + PBM, a.n_q);
+  } else if (CAUSAL) {
     const int nqb = (a.n_q + PBM - 1) / PBM;
     int qb;
     if (a.Hkv % kXcdsPP == 0) {
@@ -204,7 +261,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   const long tok = a.kv_tok_stride;
   const T* kb = reinterpret_cast<const T*>(a.k) + (long)seg_start * tok + (long)kvh * a.kv_head_stride;
   const T* vb = reinterpret_cast<const T*>(a.v) + (long)seg_start * tok + (long)kvh * a.kv_head_stride;
-  const int n_tiles = (kv_end + PBN - 1) / PBN;
+  // Tiles run t = 0 .. n_tiles-1 locally; key tile t_lo + t globally.
+  const int n_tiles = (C > 0 && CAUSAL) ? t_hi_split - t_lo : (kv_end + PBN - 1) / PBN;
 
   // Row slots interleave the groups (group 0: slots 0,2,4,6; group 1: 1,3,5,7) so both
   // groups reach the causal diagonal in the same tiles.
@@ -239,7 +297,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // LDS never holds non-finite garbage.
   auto issue_stage = [&](int u) __attribute__((always_inline)) {
     const int sl = u % PSTAGES;
-    const int tk = u * PBN, tv = (u - 1) * PBN;
+    const int tk = (t_lo + u) * PBN, tv = (t_lo + u - 1) * PBN;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int b = 2 * wave + i;
@@ -302,7 +360,9 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   float m_use = -INFINITY, l_run = 0.f;
   const float c = a.scale_log2;
 
-  auto active = [&](int t) __attribute__((always_inline)) { return !CAUSAL || t * PBN <= wpos0 + 31; };
+  auto active = [&](int t) __attribute__((always_inline)) {
+    return !CAUSAL || (t_lo + t) * PBN <= wpos0 + 31;
+  };
 
   // A operands of the MFMA phase.  K fragment (kt, s) of S^T = K . Q^T; V^T fragment
   // (chunk ck, d-tile dt) of O^T += V^T . P^T, from two transposing reads.
@@ -373,7 +433,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 
   // Softmax of S(t) into P(t) (packed 16-bit), online max / sum with lazy rescale.
   auto softmax = [&](int t) __attribute__((always_inline)) {
-    const int t0 = t * PBN;
+    const int t0 = (t_lo + t) * PBN;
     const bool need_mask = CAUSAL ? (t0 + PBN - 1 > wpos0) : (t0 + PBN > kv_end);
     if (need_mask) {
       // Key t0 + 4hf + c (c a compile-time constant below 64) is masked when it lies
@@ -495,7 +555,33 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 
   // ------------------------------------------------------------ normalise and store
-  const float inv = 1.f / (l_run + partner32(l_run));
+  const float l_tot = l_run + partner32(l_run);
+  if (partial) {
+    // Partial of this key chunk per query row: O / l rounded to T (as an output row), and
+    // (m, l) in fp32 after all items' O rows.
+    const long row = (long)blockIdx.x * PBM + (qi - q_lo);
+    if (qi < q_n) {
+      const float inv = 1.f / l_tot;
+      T* pr = reinterpret_cast<T*>(a.ws) + row * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int d0 = t * 32 + 8 * rg + 4 * hf;
+          if (d0 >= D) continue;
+          u32x2 pk = {pack2<T>(oacc[t][4 * rg] * inv, oacc[t][4 * rg + 1] * inv),
+                      pack2<T>(oacc[t][4 * rg + 2] * inv, oacc[t][4 * rg + 3] * inv)};
+          *reinterpret_cast<u32x2*>(pr + d0) = pk;
+        }
+      if (hf == 0) {
+        float* ml = a.ws + pp_ml_offset(a, D) + row * 2;
+        ml[0] = m_use;
+        ml[1] = l_tot;
+      }
+    }
+    return;
+  }
+  const float inv = 1.f / l_tot;
   if (qi < q_n) {
     T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
             (long)head * a.o_head_stride;
@@ -512,10 +598,77 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 }
 
+// Merge the key-chunk partials of the split query blocks, O = sum_c w_c O_c / sum_c w_c
+// with w_c = 2^(m_c - M) l_c.  Workgroup (head, query block, part p) gives each of its
+// threads one query row and dimensions [32p, 32p + 32); every load a thread needs (the
+// chunks' (m, l) and 64-byte row pieces) is issued before any is used.
+constexpr int kMergeMaxChunks = 8;
+template <typename T, int D>
+__global__ void __launch_bounds__(PBM) fwd_pp_merge(FwdArgs a) {
+  constexpr int NP = (D + 31) / 32;  // 32-dimension parts of a row
+  const int C = a.key_chunk_tiles;
+  const int part = (int)blockIdx.x % NP;
+  const int hb = (int)blockIdx.x / NP;
+  const int head = hb % a.Hq, qb = hb / a.Hq;
+  const int n_ch = pp_block_chunks(a, qb, C);
+  if (n_ch <= 1) return;
+  const int r = threadIdx.x;
+  const int qi = qb * PBM + r;
+  if (qi >= a.n_q) return;
+  const int nqb = (a.n_q + PBM - 1) / PBM;
+  int item0 = 0;  // the items of blocks qb+1 .. nqb-1 come first
+  for (int b = nqb - 1; b > qb; --b) item0 += pp_block_chunks(a, b, C);
+  const float* ml = a.ws + pp_ml_offset(a, D);
+  const T* po = reinterpret_cast<const T*>(a.ws);
+  const int d0 = 32 * part;
+  constexpr int NQ = 4;  // 16-byte pieces per part
+  float m[kMergeMaxChunks], l[kMergeMaxChunks];
+  Chunk<T> x[kMergeMaxChunks][NQ];
+#pragma unroll
+  for (int c = 0; c < kMergeMaxChunks; ++c) {
+    const long row = ((long)(item0 + min(c, n_ch - 1)) * a.Hq + head) * PBM + r;
+    m[c] = c < n_ch ? ml[row * 2] : -INFINITY;
+    l[c] = c < n_ch ? ml[row * 2 + 1] : 0.f;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int d = d0 + 8 * j;
+      if (c < n_ch && d < D) x[c][j] = load_chunk(po + row * D + d);
+      else x[c][j].raw = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  float M = m[0];
+#pragma unroll
+  for (int c = 1; c < kMergeMaxChunks; ++c) M = fmaxf(M, m[c]);
+  float W = 0.f, o[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) o[e] = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMergeMaxChunks; ++c) {
+    const float w = c < n_ch ? fast_exp2(m[c] - M) * l[c] : 0.f;
+    W += w;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      typedef T T8 __attribute__((ext_vector_type(8)));
+      const T8 v = __builtin_bit_cast(T8, x[c][j].raw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[8 * j + e] = __builtin_fmaf(w, (float)v[e], o[8 * j + e]);
+    }
+  }
+  const float inv = 1.f / W;
+  T* op = reinterpret_cast<T*>(a.o) + (long)qi * a.o_tok_stride + (long)head * a.o_head_stride;
+#pragma unroll
+  for (int e = 0; e < 32; e += 4) {
+    if (d0 + e >= D) break;
+    u32x2 pk = {pack2<T>(o[e] * inv, o[e + 1] * inv), pack2<T>(o[e + 2] * inv, o[e + 3] * inv)};
+    *reinterpret_cast<u32x2*>(op + d0 + e) = pk;
+  }
+}
+
 template <typename T, bool CAUSAL, int D>
 hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
   long blocks;
-  if (CAUSAL) blocks = (long)((a.n_q + PBM - 1) / PBM) * a.Hq;
+  if (CAUSAL && a.key_chunk_tiles > 0) blocks = (long)pp_items(a, a.key_chunk_tiles) * a.Hq;
+  else if (CAUSAL) blocks = (long)((a.n_q + PBM - 1) / PBM) * a.Hq;
   else blocks = (long)a.n_seg * ((a.max_seqlen + PBM - 1) / PBM) * a.Hq;
   if (blocks <= 0) return hipSuccess;
   static unsigned long long configured = 0;
@@ -530,6 +683,11 @@ hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
   }
   hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D>), dim3((unsigned)blocks), dim3(PTHREADS),
                      PLDS_BYTES, stream, a);
+  if (CAUSAL && a.key_chunk_tiles > 0) {
+    const int nqb = (a.n_q + PBM - 1) / PBM;
+    hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * ((D + 31) / 32))),
+                       dim3(PBM), 0, stream, a);
+  }
   return hipGetLastError();
 }
 
@@ -554,6 +712,26 @@ bool fwd_pp_supports(const FwdArgs& a, int dtype) {
   // K/V rows and Q/O rows are read as 16-byte chunks.
   return a.kv_tok_stride % 8 == 0 && a.kv_head_stride % 8 == 0 && a.q_tok_stride % 8 == 0 &&
          a.q_head_stride % 8 == 0;
+}
+
+int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
+  *ws_bytes = 0;
+  if (!fwd_pp_supports(a, dtype) || a.n_q <= 0 || n_cu <= 0) return 0;
+  const int nqb = (a.n_q + PBM - 1) / PBM;
+  if ((long)nqb * a.Hq >= n_cu) return 0;  // the plain launch fills the device
+  // Smallest chunk that keeps the launch to one workgroup per CU; no split if that does
+  // not shorten the longest block by at least a third.
+  const int longest = pp_block_tiles(a, nqb - 1);
+  for (int C = 1; C <= longest; ++C) {
+    if ((long)pp_items(a, C) * a.Hq > n_cu) continue;
+    if (pp_block_chunks(a, nqb - 1, C) > kMergeMaxChunks) continue;
+    const int diag_extra = longest - pp_block_diag(a, nqb - 1);
+    if (3 * (C + diag_extra) > 2 * longest) return 0;
+    const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
+    *ws_bytes = rows * a.head_size * 2 + rows * 2 * sizeof(float);
+    return C;
+  }
+  return 0;
 }
 
 hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream) {

@@ -54,6 +54,12 @@ struct FwdArgs {
   int n_seg, max_seqlen;
   int Hq, Hkv, kv_mul, head_size;
   float scale_log2;
+  // Causal key split (fwd_pp.hip): > 0 cuts each query block's keys before its diagonal
+  // into chunks of this many 64-key tiles (the diagonal tiles join the last chunk); the
+  // chunks of a block write partials to ws (normalised O rows in the input type, then
+  // fp32 (m, l)) and a second launch merges them.  0 = off.
+  int key_chunk_tiles;
+  float* ws;
 };
 
 bool fwd_supports(int dtype, int head_size);
@@ -63,6 +69,9 @@ hipError_t launch_fwd_varlen(const FwdArgs& a, int dtype, hipStream_t stream);
 // 8-wave ping-pong variant for head size 128 (fwd_pp.hip).
 bool fwd_pp_supports(const FwdArgs& a, int dtype);
 hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream);
+// Key split for a causal launch too small to fill the device with 256-query workgroups:
+// returns the chunk size in tiles (0 = no split) and the fp32 workspace bytes it needs.
+int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes);
 
 // KV-cache writes and Q/K producers (producers.hip).
 hipError_t launch_kv_append(void* cache, const void* src, const int* pos, int kv_dim,

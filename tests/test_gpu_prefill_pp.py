@@ -67,3 +67,30 @@ def test_pp_causal_small_head(kind, d):
     rows = sample_rows(S, 40, rng)
     ref = oracle.prefill_causal(0, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
     assert_lowp_close(out[rows], ref, what=f"pp causal d {d} {kind}")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("start_pos,S,Hq,Hkv", [(0, 2048, 12, 2), (100, 2049, 12, 2),
+                                                (0, 1024, 32, 8), (0, 300, 12, 2),
+                                                (37, 600, 4, 1)])
+def test_pp_causal_key_split(kind, start_pos, S, Hq, Hkv):
+    """Causal launches with fewer 256-query blocks than CUs split each block's keys before
+    its diagonal into chunks (fp32 partials merged by a second launch)
+    (S 2048, 12 q / 2 kv heads) and ragged / prefixed / tiny variants."""
+    rng = np.random.default_rng(start_pos + S + Hq)
+    d = 128
+    q, kc, vc, out = run_prefill(kind, start_pos, S, Hq, Hkv, d, start_pos + S, 1, 0, rng)
+    rows = sample_rows(S, 60, rng)
+    ref = oracle.prefill_causal(start_pos, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
+    assert_lowp_close(out[rows], ref, what=f"key split {kind} start {start_pos} S {S}")
+
+
+def test_pp_key_split_aliased_output():
+    """Output aliasing query under the key split: every chunk reads Q before the merge
+    launch writes O."""
+    rng = np.random.default_rng(77)
+    S, Hq, Hkv, d = 2048, 12, 2, 128
+    q, kc, vc, out = run_prefill("fp16", 0, S, Hq, Hkv, d, S, 1, 0, rng, alias=True)
+    rows = sample_rows(S, 60, rng)
+    ref = oracle.prefill_causal(0, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
+    assert_lowp_close(out[rows], ref, what="key split aliased")
