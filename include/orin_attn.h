@@ -98,7 +98,9 @@ int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32
  * (kuiper/source/op/kernels/cuda/flash_attention_kernel.cuh:27-80, 143-181).
  * Causal GQA prefill: query/output [seq_len, dim], caches [layers, max_seq_len, kv_dim];
  * row i attends 0..start_pos+i (flash_attention_kernel.cu:575-578).  dtype selects the
- * reference's fp32 or fp16 variant; bf16 is new.  fp16/bf16 run on MFMA.
+ * reference's fp32 or fp16 variant; bf16 is new.  fp16/bf16 run on MFMA.  A 16-bit launch
+ * with fewer 256-query blocks than the device has CUs splits the keys of each block and
+ * keeps the partials in the library-owned workspace (see orin_attn_workspace_reserve).
  */
 int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
                                  int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
