@@ -70,15 +70,15 @@ def test_pp_causal_small_head(kind, d):
 
 
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
-@pytest.mark.parametrize("start_pos,S,Hq,Hkv", [(0, 2048, 12, 2), (100, 2049, 12, 2),
-                                                (0, 1024, 32, 8), (0, 300, 12, 2),
-                                                (37, 600, 4, 1)])
-def test_pp_causal_key_split(kind, start_pos, S, Hq, Hkv):
+@pytest.mark.parametrize("start_pos,S,Hq,Hkv,d", [(0, 2048, 12, 2, 128), (100, 2049, 12, 2, 128),
+                                                  (0, 1024, 32, 8, 128), (0, 300, 12, 2, 128),
+                                                  (37, 600, 4, 1, 128), (0, 1500, 12, 12, 128),
+                                                  (5, 1800, 8, 2, 64), (0, 2048, 6, 3, 96)])
+def test_pp_causal_key_split(kind, start_pos, S, Hq, Hkv, d):
     """Causal launches with fewer 256-query blocks than CUs split each block's keys before
     its diagonal into chunks (fp32 partials merged by a second launch)
     (S 2048, 12 q / 2 kv heads) and ragged / prefixed / tiny variants."""
     rng = np.random.default_rng(start_pos + S + Hq)
-    d = 128
     q, kc, vc, out = run_prefill(kind, start_pos, S, Hq, Hkv, d, start_pos + S, 1, 0, rng)
     rows = sample_rows(S, 60, rng)
     ref = oracle.prefill_causal(start_pos, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
