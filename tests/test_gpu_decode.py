@@ -314,3 +314,27 @@ def test_gpu_pos_decode_graph_replay(kind):
         assert torch.equal(out, eager), f"replay at pos {pos} differs from eager"
         ref, _ = oracle.mha_kernel(pos, head_num, layer, max_seq, kv_dim, kv_mul, d, q, kc, vc)
         assert_lowp_close(host(out), ref, what=f"{kind} graph replay pos {pos}")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("Hq,Hkv,d", [(12, 12, 64), (12, 2, 128), (12, 4, 64), (16, 8, 256),
+                                      (28, 4, 128), (40, 5, 128), (64, 8, 128)])
+def test_decode_head_shapes(kind, Hq, Hkv, d):
+    """GQA ratios 1, 2, 3, 6, 7, 8 (query heads per workgroup G = the largest divisor of
+    kv_mul up to 8) and head sizes 64 / 128 / 256, ragged lengths, several splits."""
+    rng = np.random.default_rng(Hq * 1000 + Hkv * 10 + d)
+    B = 4
+    lens = np.array([1, 130, 700, 1500], np.int32)
+    S = int(lens.max())
+    kc = quantize(normal(rng, (B, S, Hkv, d)), kind)
+    vc = quantize(normal(rng, (B, S, Hkv, d)), kind)
+    q = quantize(normal(rng, (B, Hq, d)), kind)
+    o = torch.zeros(B, Hq, d, device="cuda", dtype=TORCH[kind])
+    K.batched_decode_cu(dev(q, kind), dev(kc, kind), dev(vc, kind), o,
+                        torch.from_numpy(lens).cuda(), S, Hkv, split_tokens=256)
+    torch.cuda.synchronize()
+    ref = oracle.decode_contig(q, kc, vc, lens)
+    if kind == "fp32":
+        assert_fp32_close(host(o), ref, d, what=f"decode {Hq}/{Hkv} d {d}")
+    else:
+        assert_lowp_close(host(o), ref, what=f"decode {Hq}/{Hkv} d {d} {kind}")
