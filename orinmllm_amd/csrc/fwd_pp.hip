@@ -1,4 +1,4 @@
-// Ping-pong attention forward for head size 128 on gfx950 (fp16 / bf16 in, fp32 accumulate).
+// Ping-pong attention forward for head sizes 64-128 on gfx950 (fp16 / bf16 in, fp32 accumulate).
 //
 // Serves the same two paths as fwd.hip (causal GQA prefill over a kuiper KV cache,
 // flash_attention_kernel.cu:554-905; bidirectional varlen attention,

@@ -66,7 +66,7 @@ bool fwd_supports(int dtype, int head_size);
 hipError_t launch_fwd_causal(const FwdArgs& a, int dtype, hipStream_t stream);
 hipError_t launch_fwd_varlen(const FwdArgs& a, int dtype, hipStream_t stream);
 
-// 8-wave ping-pong variant for head size 128 (fwd_pp.hip).
+// 8-wave ping-pong variant for head sizes 64, 72, 80, 96 and 128 (fwd_pp.hip).
 bool fwd_pp_supports(const FwdArgs& a, int dtype);
 hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream);
 // Key split for a causal launch too small to fill the device with 256-query workgroups:
