@@ -26,6 +26,14 @@
 //   with ds_read_b64_tr_b16, which transposes 16-bit elements across 16 lanes: each
 //   read hands a lane four consecutive keys of one dimension, so V^T fragments come
 //   straight from the row-major tile.
+//
+// Head sizes below 128 pad the QK contraction to a multiple of 16 (zero Q elements) and
+// O^T to a multiple of 32 (rows never stored); K/V rows keep 256-byte LDS slots.
+//
+// Key split.  A causal launch with fewer 256-query blocks than CUs is bounded by its
+// longest block; the host then cuts each block's keys before its diagonal into chunks
+// (key_chunk_tiles), each run by its own workgroup, and fwd_pp_merge combines the
+// chunks' partials (O / l in the input type, fp32 m and l) in a second launch.
 #include "common.h"
 #include "kernels.h"
 
