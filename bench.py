@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
     ap.add_argument("--no-decode-4096", action="store_true",
                     help="skip the decode with every KV length 4096")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the C1 / C2 / C3-bf16 / C5 timings")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 512 MiB device copy (the reference traffic for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -143,6 +145,71 @@ def time_decode_uniform(K, dtype, gen, pools, reps=50):
                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     del dc
     torch.cuda.empty_cache()
+    return out
+
+
+def time_other_configs(K, gen, reps=50):
+    """The other BASELINE configs on their own (parity-test shapes; not part of `value`):
+    C1 fp32 single-sequence decode, C2 fp16 causal prefill (S 2048, 12 q / 2 kv heads),
+    C3 in bf16, and C5 bf16 varlen vision attention (4 x 1024 patches, 16 heads, d 72).
+    Mean time over `reps` calls with HIP events on the current stream."""
+    import torch
+    stream = torch.cuda.current_stream()
+
+    def timeit(fn):
+        for _ in range(10):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    # C1: 12 = 12 heads, d 64, query at position 255 of a 256-row fp32 cache.
+    H, d1, seq = 12, 64, 256
+    q1 = torch.randn(H * d1, device="cuda", generator=gen)
+    k1 = torch.randn(1, seq, H * d1, device="cuda", generator=gen)
+    v1 = torch.randn_like(k1)
+    o1 = torch.empty_like(q1)
+    sc = torch.empty(H, seq, device="cuda")
+    ms = timeit(lambda: K.mha_kernel_cu(255, H, 0, seq, H * d1, 1, d1, o1, q1, sc, k1, v1))
+    kvb = 2 * seq * H * d1 * 4
+    out["c1_decode_fp32"] = {"us": round(ms * 1e3, 2), "GB/s": round(kvb / (ms * 1e-3) / 1e9, 1)}
+    # C2: causal prefill S 2048, 12 q / 2 kv heads, d 128, fp16.
+    S, Hq, Hkv, d = 2048, 12, 2, 128
+    q2 = rmsnorm_rope(torch.randn(S, Hq * d, device="cuda", generator=gen), Hq, d).half()
+    k2 = rmsnorm_rope(torch.randn(S, Hkv * d, device="cuda", generator=gen), Hkv, d).half()
+    v2 = torch.randn(S, Hkv * d, device="cuda", generator=gen).half()
+    o2 = torch.empty_like(q2)
+    ms = timeit(lambda: K.flash_attention_prefill_cu(0, S, Hq, Hkv, d, Hq // Hkv, 0, S, Hkv * d,
+                                                     q2, o2, k2, v2))
+    fl = 4.0 * d * Hq * S * (S + 1) / 2
+    tf = fl / (ms * 1e-3) / 1e12
+    out["c2_prefill_fp16"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                              "frac_mfma": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    # C3 in bf16.
+    pf = make_prefill(torch.bfloat16, gen)
+    ms = timeit(lambda: K.flash_attention_prefill_cu(0, pf["S"], pf["Hq"], pf["Hkv"], pf["d"],
+                                                     pf["Hq"] // pf["Hkv"], 0, pf["S"],
+                                                     pf["Hkv"] * pf["d"], pf["q"], pf["o"],
+                                                     pf["k"], pf["v"]))
+    tf = pf["flops"] / (ms * 1e-3) / 1e12
+    out["c3_prefill_bf16"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                              "frac_mfma": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    # C5: bf16 vision, 4 images x 1024 patches, 16 heads, d 72, bidirectional.
+    Hv, dv, N = 16, 72, 4096
+    qv, kv, vv = (torch.randn(Hv, N, dv, device="cuda", generator=gen).bfloat16()
+                  for _ in range(3))
+    ov = torch.empty(N, Hv * dv, device="cuda", dtype=torch.bfloat16)
+    cu = torch.tensor([0, 1024, 2048, 3072, 4096], dtype=torch.int32, device="cuda")
+    ms = timeit(lambda: K.vision_attention_varlen_cu(qv, kv, vv, ov, cu, 1024, Hv, dv))
+    fl = 4.0 * 4 * 1024 * 1024 * dv * Hv
+    tf = fl / (ms * 1e-3) / 1e12
+    out["c5_vision_bf16"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                             "frac_mfma": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
     return out
 
 
@@ -375,6 +442,8 @@ def main():
     }
     if not args.no_decode_4096:
         out["decode_kv4096"] = time_decode_uniform(K, dtype, gen, args.pools)
+    if not args.no_other_configs:
+        out["other_configs"] = time_other_configs(K, gen)
     if not args.no_producers:
         out["producers"] = time_producers(K, make_producers(dtype, gen))
         for name, rec in out["producers"].items():
