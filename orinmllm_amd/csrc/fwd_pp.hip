@@ -201,6 +201,29 @@ struct PhaseOrder {
   }
 };
 
+// Scheduling pins for one MFMA phase: the LDS reads of the first PF fragments, then per MFMA
+// i the MFMA and the reads of fragment i + PF (one ds_read_b128 for a K fragment, two
+// ds_read_b64_tr_b16 for a V fragment).  Without them the compiler sinks each read to just
+// before its MFMA, which then waits out most of the LDS latency.
+template <int NQK, int NPV, int I>
+__device__ __forceinline__ void sgb_seq() {
+  constexpr int N = NQK + NPV;
+  if constexpr (I < N) {
+    constexpr PhaseOrder<NQK, NPV> o{};
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (I + PF < N) __builtin_amdgcn_sched_group_barrier(0x100, o.is_qk[I + PF] ? 1 : 2, 0);
+    sgb_seq<NQK, NPV, I + 1>();
+  }
+}
+template <int NQK, int NPV, int I>
+__device__ __forceinline__ void sgb_head() {
+  if constexpr (I < PF) {
+    constexpr PhaseOrder<NQK, NPV> o{};
+    __builtin_amdgcn_sched_group_barrier(0x100, o.is_qk[I] ? 1 : 2, 0);
+    sgb_head<NQK, NPV, I + 1>();
+  }
+}
+
 template <typename T, bool CAUSAL, int D>
 __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   static_assert(D % 8 == 0 && D <= PD, "head size: a multiple of 8 up to 128");
@@ -437,6 +460,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
         oacc[n % DT] = mfma32<T>(fr[i % (PF + 1)], pf[n / DT], oacc[n % DT]);
       }
     }
+    sgb_head<NQK, NPV, 0>();
+    sgb_seq<NQK, NPV, 0>();
   };
 
   // Softmax of S(t) into P(t) (packed 16-bit), online max / sum with lazy rescale.
