@@ -128,6 +128,15 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
                    : "memory", "m0");
 }
 
+// The same transfer from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset:
+// the per-tile address arithmetic stays on the scalar unit.
+__device__ __forceinline__ void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(voff), "s"(sbase), "s"(lds_addr)
+                   : "memory", "m0");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
@@ -326,18 +335,30 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // Stage u = K(u) + V(u-1) into ring slot u % 3.  Rows past the sequence (and V(-1))
   // read a valid row instead, so every stage is exactly four transfers per wave and
   // LDS never holds non-finite garbage.
+  // Addresses: a wave-uniform tile base (scalar) plus a per-lane byte offset
+  // row_in_tile * row_bytes + column bytes (`fwd_pp_supports` keeps row_bytes below 2^24,
+  // so one 24-bit multiply-add forms it).
+  const uint32_t row_bytes = (uint32_t)tok * sizeof(T);
   auto issue_stage = [&](int u) __attribute__((always_inline)) {
     const int sl = u % PSTAGES;
-    const int tk = (t_lo + u) * PBN, tv = (t_lo + u - 1) * PBN;
+    // Tile bases are clamped into [0, kv_end - 1] so that the last valid row's offset from
+    // its base is never negative: K(n_tiles) of the last stage starts past the sequence and
+    // V(-1) before it; every row of such a tile reads a valid row.
+    const int tk = (t_lo + u) * PBN, tv = tk - PBN;
+    const int tk0 = tk < kv_end - 1 ? tk : kv_end - 1;
+    const int tv0 = tv < 0 ? 0 : (tv < kv_end - 1 ? tv : kv_end - 1);
+    const char* kt_base = reinterpret_cast<const char*>(kb + (long)tk0 * tok);
+    const char* vt_base = reinterpret_cast<const char*>(vb + (long)tv0 * tok);
+    const int k_last = kv_end - 1 - tk0, v_last = kv_end - 1 - tv0;  // >= 0
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int b = 2 * wave + i;
-      int rk = tk + k_row[i];
-      rk = rk < kv_end ? rk : kv_end - 1;
-      int rv = tv + k_row[i];
-      rv = rv < 0 ? k_row[i] : (rv < kv_end ? rv : kv_end - 1);
-      dma16(kb + (long)rk * tok + k_col[i], k_base + sl * PTILE_BYTES + b * 1024);
-      dma16(vb + (long)rv * tok + v_col[i], k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
+      const int rk = k_row[i] < k_last ? k_row[i] : k_last;
+      const int rv = k_row[i] < v_last ? k_row[i] : v_last;
+      dma16_s(kt_base, __umul24(rk, row_bytes) + k_col[i] * (uint32_t)sizeof(T),
+              k_base + sl * PTILE_BYTES + b * 1024);
+      dma16_s(vt_base, __umul24(rv, row_bytes) + v_col[i] * (uint32_t)sizeof(T),
+              k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
     }
   };
 
@@ -743,8 +764,9 @@ bool fwd_pp_supports(const FwdArgs& a, int dtype) {
   if (!(d == 64 || d == 72 || d == 80 || d == 96 || d == 128) || !(dtype == kF16 || dtype == kBF16))
     return false;
   // K/V rows and Q/O rows are read as 16-byte chunks.
+  // K/V transfer offsets within a tile are formed with 24-bit multiplies.
   return a.kv_tok_stride % 8 == 0 && a.kv_head_stride % 8 == 0 && a.q_tok_stride % 8 == 0 &&
-         a.q_head_stride % 8 == 0;
+         a.q_head_stride % 8 == 0 && a.kv_tok_stride * 2 < (1 << 24);
 }
 
 int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
