@@ -10,6 +10,7 @@
 #ifndef ORIN_HOST_KERNELS_H
 #define ORIN_HOST_KERNELS_H
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
@@ -107,7 +108,7 @@ void fused_split_rope_transpose_cu(const tensor::Tensor& qkv, const tensor::Tens
 void copy_to_kv_cache_kernel(float* kv_cache, const float* src, const int32_t* pos,
                              int32_t kv_dim, int32_t layer_idx, int32_t seq_len,
                              hipStream_t stream);
-void copy_to_kv_cache_kernel_fp16(_Float16* kv_cache, const _Float16* src, const int32_t* pos,
+void copy_to_kv_cache_kernel_fp16(__half* kv_cache, const __half* src, const int32_t* pos,
                                   int32_t kv_dim, int32_t layer_idx, int32_t seq_len,
                                   hipStream_t stream);
 void sin_cos_cache_calc_cu(int head_size, int max_seq_len, const tensor::Tensor& sin_cache,

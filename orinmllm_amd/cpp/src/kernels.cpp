@@ -201,7 +201,7 @@ void copy_to_kv_cache_kernel(float* kv_cache, const float* src, const int32_t* p
                                static_cast<void*>(stream)));
 }
 
-void copy_to_kv_cache_kernel_fp16(_Float16* kv_cache, const _Float16* src, const int32_t* pos,
+void copy_to_kv_cache_kernel_fp16(__half* kv_cache, const __half* src, const int32_t* pos,
                                   int32_t kv_dim, int32_t layer_idx, int32_t seq_len,
                                   hipStream_t stream) {
   record("copy_to_kv_cache_kernel_fp16",

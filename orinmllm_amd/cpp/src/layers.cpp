@@ -245,7 +245,7 @@ Status CopyToKVCacheLayer::forward(const tensor::Tensor& kv_cache, const tensor:
                                    int32_t seq_len) {
   hipStream_t s = cuda_config_ ? cuda_config_->stream : nullptr;
   if (kv_cache.data_type() == base::DataType::kDataTypeFp16)
-    kernel::copy_to_kv_cache_kernel_fp16(kv_cache.ptr<_Float16>(), kv_data.ptr<const _Float16>(),
+    kernel::copy_to_kv_cache_kernel_fp16(kv_cache.ptr<__half>(), kv_data.ptr<const __half>(),
                                          pos_gpu, kv_dim, layer_idx, seq_len, s);
   else
     kernel::copy_to_kv_cache_kernel(kv_cache.ptr<float>(), kv_data.ptr<const float>(), pos_gpu,
