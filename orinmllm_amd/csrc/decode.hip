@@ -443,6 +443,16 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   const int nsplit = len > 0 ? (len + a.split_tokens - 1) / a.split_tokens : 0;
   if (nsplit <= 1) return;
   const float* ph = a.ws + ((long)row * a.Hq + h) * a.max_splits * (D + 2);
+  const float* pl = ph + threadIdx.x * EPL;
+  // The first kFirst partial rows are loaded before (m, l), so both memory round trips
+  // overlap instead of running one after the other.
+  constexpr int kFirst = 16;
+  float x0[kFirst][EPL];
+#pragma unroll
+  for (int u = 0; u < kFirst; ++u)
+    if (u < nsplit)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x0[u][e] = pl[u * (D + 2) + e];
   __shared__ float s_m[kMaxCombineSplits], s_l[kMaxCombineSplits];
   float M = -INFINITY;
   for (int sp = threadIdx.x; sp < nsplit; sp += kWave) {
@@ -457,8 +467,15 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   float L = 0.f, o[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) o[e] = 0.f;
-  const float* pl = ph + threadIdx.x * EPL;
-  int sp = 0;
+#pragma unroll
+  for (int u = 0; u < kFirst; ++u)
+    if (u < nsplit) {
+      const float f = fast_exp2(s_m[u] - M);
+      L = __builtin_fmaf(f, s_l[u], L);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[e] = __builtin_fmaf(f, x0[u][e], o[e]);
+    }
+  int sp = kFirst;
   for (; sp + 8 <= nsplit; sp += 8) {
     float x[8][EPL];
 #pragma unroll
