@@ -653,20 +653,24 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 }
 
 // Merge the key-chunk partials of the split query blocks, O = sum_c w_c O_c / sum_c w_c
-// with w_c = 2^(m_c - M) l_c.  Workgroup (head, query block, part p) gives each of its
-// threads one query row and dimensions [32p, 32p + 32); every load a thread needs (the
-// chunks' (m, l) and 64-byte row pieces) is issued before any is used.
+// with w_c = 2^(m_c - M) l_c.  Workgroup (head, query block, 64-row quarter) gives each
+// row ceil(D/32) neighbouring threads, thread p of a row covering dimensions
+// [32p, 32p + 32); every load a thread needs (the chunks' (m, l) and 64-byte row pieces)
+// is issued before any is used.
 constexpr int kMergeMaxChunks = 8;
 template <typename T, int D>
 __global__ void __launch_bounds__(PBM) fwd_pp_merge(FwdArgs a) {
   constexpr int NP = (D + 31) / 32;  // 32-dimension parts of a row
   const int C = a.key_chunk_tiles;
-  const int part = (int)blockIdx.x % NP;
-  const int hb = (int)blockIdx.x / NP;
+  // Workgroup: 64 rows of one (block, head), NP neighbouring threads per row, so a wave's
+  // loads cover whole rows.
+  const int quarter = (int)blockIdx.x % (PBM / 64);
+  const int hb = (int)blockIdx.x / (PBM / 64);
   const int head = hb % a.Hq, qb = hb / a.Hq;
   const int n_ch = pp_block_chunks(a, qb, C);
   if (n_ch <= 1) return;
-  const int r = threadIdx.x;
+  const int part = (int)threadIdx.x % NP;
+  const int r = quarter * 64 + (int)threadIdx.x / NP;
   const int qi = qb * PBM + r;
   if (qi >= a.n_q) return;
   const int nqb = (a.n_q + PBM - 1) / PBM;
@@ -739,8 +743,8 @@ hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
                      PLDS_BYTES, stream, a);
   if (CAUSAL && a.key_chunk_tiles > 0) {
     const int nqb = (a.n_q + PBM - 1) / PBM;
-    hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * ((D + 31) / 32))),
-                       dim3(PBM), 0, stream, a);
+    hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * (PBM / 64))),
+                       dim3(64 * ((D + 31) / 32)), 0, stream, a);
   }
   return hipGetLastError();
 }
