@@ -306,3 +306,65 @@ def test_bf16_rounding_matches_torch():
     ours = oracle.round_bf16(x)
     ref = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
     assert np.array_equal(ours, ref)
+
+
+def test_vision_rotary_direction_closed_form():
+    """Pin the rotation direction (vision_encoder_kernel.cu:715-718): with x1 = 1, x2 = 0
+    the pair becomes (c, s); with x1 = 0, x2 = 1 it becomes (-s, c).  A reversed rotation
+    (x1*c + x2*s) keeps the pair norms and would pass a norm check, not this one."""
+    d, N = 8, 3
+    half = d // 2
+    ang = np.array([0.3, np.pi / 2, -1.1], np.float64)
+    c = np.repeat(np.cos(ang)[:, None], d, 1).astype(np.float32)
+    s = np.repeat(np.sin(ang)[:, None], d, 1).astype(np.float32)
+    x = np.zeros((2, N, d), np.float32)
+    x[0, :, :half] = 1.0  # unit x1
+    x[1, :, half:] = 1.0  # unit x2
+    y = oracle.vision_rotary(x, c, s)
+    for t in range(N):
+        assert np.allclose(y[0, t, :half], np.cos(ang[t]), atol=1e-6)
+        assert np.allclose(y[0, t, half:], np.sin(ang[t]), atol=1e-6)
+        assert np.allclose(y[1, t, :half], -np.sin(ang[t]), atol=1e-6)
+        assert np.allclose(y[1, t, half:], np.cos(ang[t]), atol=1e-6)
+    # 90 degrees: (1, 0) -> (0, 1)
+    assert np.allclose(y[0, 1, :half], 0.0, atol=1e-6) and np.allclose(y[0, 1, half:], 1.0)
+    # the two halves use their own table entries (cos[j] / sin[j] for x1',
+    # sin[j + d/2] / cos[j + d/2] for x2'): distinct tables per half are honoured
+    c2 = np.ones((1, d), np.float32)
+    s2 = np.zeros((1, d), np.float32)
+    c2[0, half:] = 0.0
+    s2[0, half:] = 1.0  # x2' = x1 * 1 + x2 * 0
+    xx = np.arange(d, dtype=np.float32).reshape(1, 1, d) + 1.0
+    yy = oracle.vision_rotary(xx, c2, s2)[0, 0]
+    assert np.allclose(yy[:half], xx[0, 0, :half]) and np.allclose(yy[half:], xx[0, 0, :half])
+
+
+def test_vision_cos_sin_all_frequencies():
+    """Every entry of the [h, w, h, w] tables against an independent float64 evaluation of
+    qwen3_vl.cpp:1741-1812: inv_freq[j] = 10000^(-2j/(d/2)), j < d/4, with (h, w) taken
+    from the 2x2 merge-block token order.  A wrong exponent (2j/d) or swapped quarters
+    fails here at j > 0."""
+    d, gh, gw, merge = 72, 6, 4, 2
+    q4, half = d // 4, d // 2
+    c, s = oracle.vision_cos_sin(1, gh, gw, merge, d)
+    pos = []
+    for bh in range(gh // merge):
+        for bw in range(gw // merge):
+            for lh in range(merge):
+                for lw in range(merge):
+                    pos.append((bh * merge + lh, bw * merge + lw))
+    j = np.arange(q4, dtype=np.float64)
+    inv = 10000.0 ** (-2.0 * j / half)
+    for t, (h, w) in enumerate(pos):
+        exp_c = np.concatenate([np.cos(h * inv), np.cos(w * inv)] * 2)
+        exp_s = np.concatenate([np.sin(h * inv), np.sin(w * inv)] * 2)
+        assert np.allclose(c[t], exp_c, atol=2e-6), t
+        assert np.allclose(s[t], exp_s, atol=2e-6), t
+    # spot values named in the reference's comments: token (h=0, w=1) is index 1
+    t1 = pos.index((0, 1))
+    for jj in (1, q4 - 1):
+        assert np.isclose(c[t1, q4 + jj], np.cos(10000.0 ** (-2.0 * jj / half)), atol=1e-6)
+    t2 = pos.index((1, 0))
+    for jj in (1, q4 - 1):
+        assert np.isclose(c[t2, jj], np.cos(10000.0 ** (-2.0 * jj / half)), atol=1e-6)
+        assert np.isclose(s[t2, half + jj], np.sin(10000.0 ** (-2.0 * jj / half)), atol=1e-6)
