@@ -8,8 +8,9 @@ decode (config 4: 32 q / 8 kv heads, d 128, KV lengths U[512, 4096], block 16, f
 call); the decode KV-read bandwidth (4096 * sum(L) bytes per call) is reported under
 `decode`.  Inputs are synthetic and resident in HBM before timing starts.  The decode
 reads one of several KV pools in rotation so that the 256 MB last-level cache does not
-serve it.  Each kernel's mean launch time is measured with HIP events on the stream the
-kernels run on; `ms_per_step` is the wall time of the K timed steps.
+serve it.  Each kernel's time is the median of at least 50 launches, each bracketed by
+its own pair of HIP events on the stream the kernels run on, after at least 10 warmups
+(the mean is reported beside it); `ms_per_step` is the wall time of the K timed steps.
 
 The CPU baseline runs the oracle (oracle/oracle.c, a restatement of the reference's CPU
 MHA) on a bounded sample of the same workload on the host cores.
@@ -46,6 +47,10 @@ def parse():
     ap.add_argument("--no-producers", action="store_true",
                     help="skip the timing of the KV-write / Q-K producer kernels")
     ap.add_argument("--pools", type=int, default=4, help="KV pools rotated by the decode")
+    ap.add_argument("--reps", type=int, default=100,
+                    help="per-launch timings behind the reported medians (at least 50 used)")
+    ap.add_argument("--kernel-warmup", type=int, default=10,
+                    help="untimed launches before the per-launch timings (at least 10 used)")
     ap.add_argument("--no-decode-4096", action="store_true",
                     help="skip the decode with every KV length 4096")
     ap.add_argument("--no-other-configs", action="store_true",
@@ -131,15 +136,7 @@ def time_decode_uniform(K, dtype, gen, pools, reps=50):
                               dc["lens_d"], dc["maxlen"], split_tokens=st, workspace=ws,
                               layout=dc["layout"])
 
-        for i in range(10):
-            run(i)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(reps):
-            run(i)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
+        ms = per_launch(run, reps, 10, stream, indexed=True)["median_ms"]
         gbs = dc["kv_bytes"] / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -152,20 +149,12 @@ def time_other_configs(K, gen, reps=50):
     """The other BASELINE configs on their own (parity-test shapes; not part of `value`):
     C1 fp32 single-sequence decode, C2 fp16 causal prefill (S 2048, 12 q / 2 kv heads),
     C3 in bf16, and C5 bf16 varlen vision attention (4 x 1024 patches, 16 heads, d 72).
-    Mean time over `reps` calls with HIP events on the current stream."""
+    Median time over `reps` calls, each bracketed by HIP events on the current stream."""
     import torch
     stream = torch.cuda.current_stream()
 
     def timeit(fn):
-        for _ in range(10):
-            fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
+        return per_launch(fn, reps, 10, stream)["median_ms"]
 
     out = {}
     # C1: 12 = 12 heads, d 64, query at position 255 of a 256-row fp32 cache.
@@ -253,7 +242,7 @@ def make_producers(dtype, gen):
 
 
 def time_producers(K, p, reps=50):
-    """Mean time (HIP events on the stream the kernels run on) and HBM GB/s of each."""
+    """Median time (per-launch HIP events on the stream the kernels run on) and HBM GB/s."""
     import torch
     from orinmllm_amd import _lib
     S, Hq, Hkv, d, N, H, dv = p["shape"]
@@ -279,20 +268,39 @@ def time_producers(K, p, reps=50):
     stream = torch.cuda.current_stream()
     out = {}
     for name, (fn, nbytes) in calls.items():
-        for _ in range(5):
-            fn()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
+        ms = per_launch(fn, reps, 10, stream)["median_ms"]
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     return out
+
+
+def per_launch(fn, reps, warmup, stream, indexed=False):
+    """Median and mean of `reps` launches of fn, each bracketed by its own pair of HIP
+    events on `stream`, after `warmup` untimed launches.  A short device-side spin is
+    queued first so the host runs ahead of the device and the event pairs do not include
+    host launch time."""
+    import statistics
+
+    import torch
+    call = (lambda i: fn(i)) if indexed else (lambda i: fn())
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    try:
+        torch.cuda._sleep(20_000_000)
+    except Exception:
+        pass
+    for i, (a, b) in enumerate(ev):
+        a.record(stream)
+        call(warmup + i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ts = [a.elapsed_time(b) for a, b in ev]
+    return {"median_ms": round(statistics.median(ts), 5), "mean_ms": round(sum(ts) / len(ts), 5),
+            "min_ms": round(min(ts), 5), "max_ms": round(max(ts), 5)}
 
 
 def cpu_baseline(pf, dc, min_seconds=8.0):
@@ -359,6 +367,8 @@ def cpu_baseline(pf, dc, min_seconds=8.0):
 
 def main():
     args = parse()
+    args.reps = max(args.reps, 50)
+    args.kernel_warmup = max(args.kernel_warmup, 10)
     traffic = {}
     tpath = os.path.join(REPO, "profiles", "traffic.json")
     if os.path.exists(tpath):
@@ -410,8 +420,13 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
-    pf_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    dc_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    step_pf_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    step_dc_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    # Per-kernel figures: median of >= 50 per-launch event pairs after >= 10 warmups.
+    reps = max(args.reps, args.steps)
+    pf_t = per_launch(prefill, reps, args.kernel_warmup, stream)
+    dc_t = per_launch(lambda i: decode(i), reps, args.kernel_warmup, stream, indexed=True)
+    pf_ms, dc_ms = pf_t["median_ms"], dc_t["median_ms"]
     pf_tflops = pf["flops"] / (pf_ms * 1e-3) / 1e12
     dc_gbs = dc["kv_bytes"] / (dc_ms * 1e-3) / 1e9
 
@@ -433,6 +448,13 @@ def main():
                         "B=32 Hq=32 Hkv=8 d=128 L~U[512,4096] block 16",
             "prefill_ms": round(pf_ms, 4),
             "decode_ms": round(dc_ms, 4),
+            "timing": {
+                "value_is": "median over per-launch HIP event pairs",
+                "reps": reps, "warmup": args.kernel_warmup,
+                "prefill": pf_t, "decode": dc_t,
+                "timed_steps_mean_ms": {"prefill": round(step_pf_ms, 4),
+                                        "decode": round(step_dc_ms, 4)},
+            },
             "kv_pools_rotated": args.pools,
             "traffic_source": traffic.get("source"),
         },

@@ -100,7 +100,7 @@ int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32
  * row i attends 0..start_pos+i (flash_attention_kernel.cu:575-578).  dtype selects the
  * reference's fp32 or fp16 variant; bf16 is new.  fp16/bf16 run on MFMA.  A 16-bit launch
  * with fewer 256-query blocks than the device has CUs splits the keys of each block and
- * keeps the partials in the library-owned workspace (see orin_attn_workspace_reserve).
+ * keeps the partials in the stream's library-owned workspace (see below).
  */
 int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
                                  int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
@@ -112,8 +112,8 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
  * kernel::flash_attention_decode_cu / flash_attention_decode_fp16_cu /
  * flash_attention2_decode_cu / flash_attention2_decode_fp16_cu
  * (flash_attention_kernel.cuh:50-63, 84-97, 186-216).  One query row [dim] at
- * position pos over cache rows 0..pos.  Split-KV partials go to a workspace owned
- * by this library (grown on demand per device; see orin_attn_workspace_reserve).
+ * position pos over cache rows 0..pos.  Split-KV partials go to the stream's
+ * library-owned workspace (see orin_attn_workspace_reserve_stream).
  */
 int orin_flash_attention_decode(int32_t pos, int32_t head_num, int32_t kv_head_num,
                                 int32_t head_size, int32_t kv_mul, int32_t layer_index,
@@ -125,7 +125,7 @@ int orin_flash_attention_decode(int32_t pos, int32_t head_num, int32_t kv_head_n
  * kernel::flash_attention_decode_fp16_gpu_pos_cu / flash_attention2_decode_fp16_gpu_pos_cu
  * (flash_attention_kernel.cuh:103-117, 222-234): the decode above with the position
  * read from device memory (HIP-graph capturable).  The launch shape and workspace
- * depend only on max_seq_len; reserve the workspace before capturing.
+ * depend only on max_seq_len; reserve the capture stream's workspace before capturing.
  */
 int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num,
                                         int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
@@ -133,12 +133,37 @@ int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num
                                         const void* query, void* output, const void* key_cache,
                                         const void* value_cache, int32_t dtype, void* stream);
 
-/* Bytes of library-owned workspace the flash decode entry points need for a cache
- * of max_seq_len rows, and a call that allocates it on the current device now (so
- * that a later graph capture does not allocate). */
+/*
+ * Library-owned workspaces (no reference counterpart: kuiper's flash decode and prefill
+ * take no workspace argument).  The flash decode entry points and the key split of a
+ * small causal prefill keep their partials in buffers owned by this library, one per
+ * (device, stream, use): calls on different streams never share bytes, so the entry
+ * points are reentrant across streams; calls on one stream are ordered by it.
+ *  - A buffer grows on demand (hipMalloc, no synchronisation).  The buffer it replaces is
+ *    kept allocated, because a captured graph may still use its address, until
+ *    orin_attn_workspace_release.
+ *  - While `stream` is being captured nothing is allocated: a call whose buffer is missing
+ *    or too small returns ORIN_ERR_WORKSPACE.  Reserve before capturing.
+ *  - A graph uses the buffer of the stream it was captured on: do not replay it while
+ *    other work that uses that stream's buffer runs.
+ *
+ * orin_flash_attention_decode_workspace_size: decode bytes for a cache of max_seq_len rows
+ * (any kv_head_num).  orin_flash_attention_prefill_workspace_size: key-split bytes of one
+ * causal prefill launch (0 when it does not split).  orin_attn_workspace_reserve_stream
+ * allocates both on the current device for `stream` now.  orin_attn_workspace_reserve
+ * reserves decode bytes for the NULL stream and makes every decode buffer created later on
+ * this device at least that large.  orin_attn_workspace_release synchronises the device and
+ * frees every library-owned buffer of the current device; call it only when no captured
+ * graph that used them will be replayed.
+ */
 size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head_size,
                                                   int32_t max_seq_len);
+size_t orin_flash_attention_prefill_workspace_size(int32_t start_pos, int32_t seq_len,
+                                                   int32_t head_num, int32_t kv_head_num,
+                                                   int32_t head_size, int32_t dtype);
 int orin_attn_workspace_reserve(size_t bytes);
+int orin_attn_workspace_reserve_stream(size_t decode_bytes, size_t prefill_bytes, void* stream);
+int orin_attn_workspace_release(void);
 
 /* ------------------------------------------------------------------ batched decode */
 
@@ -149,7 +174,9 @@ int orin_attn_workspace_reserve(size_t bytes);
  * sequence b's token t, kv head g lives at
  *   cache + b*cache_batch_stride + t*cache_tok_stride + g*head_size   (elements).
  * context_lens (device, [batch]) gives each row's KV length; max_context_len bounds
- * them (it sets the launch shape).  split_tokens: tokens per split (multiple of 64,
+ * them (it sets the launch shape).  A row whose length exceeds max_context_len (the host
+ * cannot see device lengths) gets NaN outputs instead of attention over a truncated
+ * prefix; the same holds for *pos_ptr >= max_seq_len in the gpu-pos entry points.  split_tokens: tokens per split (multiple of 64,
  * else ORIN_ERR_INVALID_ARG), 0 = automatic.  Workspace: orin_attn_decode_workspace_size bytes (may be NULL when
  * that is 0).
  */

@@ -36,7 +36,10 @@ SIGNATURES = {
     "orin_flash_attention_decode": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode_gpu_pos": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode_workspace_size": (sz, [i32, i32, i32]),
+    "orin_flash_attention_prefill_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "orin_attn_workspace_reserve": (C.c_int, [sz]),
+    "orin_attn_workspace_reserve_stream": (C.c_int, [sz, sz, vp]),
+    "orin_attn_workspace_release": (C.c_int, []),
     "orin_attn_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "orin_attn_decode_split_tokens": (i32, [i32, i32, i32, i32, i32]),
     "orin_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, i64, i64, vp, i32, i32, f32, i32, vp, sz, vp]),

@@ -65,33 +65,71 @@ bool heads_ok(int head_num, int kv_head_num, int kv_mul) {
   return head_num > 0 && kv_head_num > 0 && kv_mul > 0 && head_num == kv_head_num * kv_mul;
 }
 
-// Library-owned workspace, one grow-only buffer per device.
-std::mutex g_ws_mu;
-std::vector<std::pair<void*, size_t>> g_ws;
+// Library-owned workspaces.  The kuiper-shaped flash decode and the causal prefill key
+// split take no workspace argument, so the library keeps one grow-only buffer per
+// (device, stream, kind): calls on different streams never share bytes, and the decode
+// partials never share a buffer with the prefill key split.  A buffer that has to grow is
+// retired, not freed: a captured graph may still hold its address, so it stays allocated
+// until orin_attn_workspace_release.  Nothing here synchronises a stream or the device,
+// and a stream that is capturing gets ORIN_ERR_WORKSPACE instead of an allocation.
+enum WsKind { kWsDecode = 0, kWsPrefillSplit = 1 };
 
-int library_workspace(size_t bytes, void** out) {
+struct WsSlot {
+  int dev;
+  void* stream;
+  int kind;
+  void* ptr;
+  size_t bytes;
+};
+
+std::mutex g_ws_mu;
+std::vector<WsSlot> g_ws;                          // live buffers
+std::vector<std::pair<int, void*>> g_ws_retired;   // (device, buffer) kept for graphs
+std::vector<size_t> g_ws_floor;                    // per device: minimum decode buffer size
+
+// Grow geometrically so that a sequence of slightly larger calls retires few buffers.
+size_t grown_size(size_t have, size_t need) {
+  size_t n = have ? have : 1;
+  while (n < need) n *= 2;
+  return n < need ? need : n;
+}
+
+int library_workspace(int kind, hipStream_t stream, size_t bytes, void** out) {
   *out = nullptr;
   if (bytes == 0) return ORIN_OK;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_status(e);
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1, {nullptr, 0});
-  auto& slot = g_ws[dev];
-  if (slot.second < bytes) {
-    if (slot.first) {
-      // Earlier launches may still read the old buffer.
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return hip_status(e);
-      (void)hipFree(slot.first);
-      slot = {nullptr, 0};
-    }
-    void* p = nullptr;
-    e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return hip_status(e);
-    slot = {p, bytes};
+  WsSlot* slot = nullptr;
+  for (auto& w : g_ws)
+    if (w.dev == dev && w.stream == (void*)stream && w.kind == kind) slot = &w;
+  if (slot && slot->bytes >= bytes) {
+    *out = slot->ptr;
+    return ORIN_OK;
   }
-  *out = slot.first;
+  // Allocation needed: refuse while this stream is being captured (the caller reserves
+  // with orin_attn_workspace_reserve_stream before capturing).
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (stream != nullptr) {
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_status(e);
+  }
+  if (cs != hipStreamCaptureStatusNone) return ORIN_ERR_WORKSPACE;
+  size_t want = grown_size(slot ? slot->bytes : 0, bytes);
+  if (kind == kWsDecode && dev < (int)g_ws_floor.size() && g_ws_floor[dev] > want)
+    want = g_ws_floor[dev];
+  void* p = nullptr;
+  e = hipMalloc(&p, want);
+  if (e != hipSuccess) return hip_status(e);
+  if (slot) {
+    g_ws_retired.push_back({dev, slot->ptr});
+    slot->ptr = p;
+    slot->bytes = want;
+  } else {
+    g_ws.push_back({dev, (void*)stream, kind, p, want});
+  }
+  *out = p;
   return ORIN_OK;
 }
 
@@ -156,8 +194,50 @@ const char* orin_attn_status_string(int status) {
 const char* orin_attn_last_hip_error(void) { return g_last_hip_error.c_str(); }
 
 int orin_attn_workspace_reserve(size_t bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if ((int)g_ws_floor.size() <= dev) g_ws_floor.resize(dev + 1, 0);
+    if (g_ws_floor[dev] < bytes) g_ws_floor[dev] = bytes;
+  }
   void* p;
-  return library_workspace(bytes, &p);
+  return library_workspace(kWsDecode, nullptr, bytes, &p);
+}
+
+int orin_attn_workspace_reserve_stream(size_t decode_bytes, size_t prefill_bytes, void* stream) {
+  void* p;
+  int st = library_workspace(kWsDecode, (hipStream_t)stream, decode_bytes, &p);
+  if (st != ORIN_OK) return st;
+  return library_workspace(kWsPrefillSplit, (hipStream_t)stream, prefill_bytes, &p);
+}
+
+int orin_attn_workspace_release(void) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_status(e);
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (auto it = g_ws.begin(); it != g_ws.end();) {
+    if (it->dev == dev) {
+      (void)hipFree(it->ptr);
+      it = g_ws.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  for (auto it = g_ws_retired.begin(); it != g_ws_retired.end();) {
+    if (it->first == dev) {
+      (void)hipFree(it->second);
+      it = g_ws_retired.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  if (dev < (int)g_ws_floor.size()) g_ws_floor[dev] = 0;
+  return ORIN_OK;
 }
 
 // ------------------------------------------------------------------ fp32 MHA
@@ -316,7 +396,7 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
   const int chunk = fwd_pp_key_split(a, dtype, device_cus(), &split_bytes);
   if (chunk > 0) {
     void* ws = nullptr;
-    const int st = library_workspace(split_bytes, &ws);
+    const int st = library_workspace(kWsPrefillSplit, (hipStream_t)stream, split_bytes, &ws);
     if (st != ORIN_OK) return st;
     a.key_chunk_tiles = chunk;
     a.ws = static_cast<float*>(ws);
@@ -340,7 +420,8 @@ static int flash_decode_common(int32_t pos, const int32_t* pos_ptr, int32_t head
   a.split_tokens = kuiper_decode_split(head_num, kv_head_num, head_size, max_len, 0, false);
   const int splits = n_splits(max_len, a.split_tokens);
   void* ws = nullptr;
-  int st = library_workspace(ws_bytes(1, head_num, head_size, splits), &ws);
+  int st = library_workspace(kWsDecode, (hipStream_t)stream, ws_bytes(1, head_num, head_size, splits),
+                             &ws);
   if (st != ORIN_OK) return st;
   const size_t layer_off = (size_t)layer_index * max_seq_len * kv_dim * elem_size(dtype);
   a.q = query;
@@ -397,6 +478,27 @@ size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head
   // so size for kv_head_num = 1.
   const int st = auto_split_tokens(decode_base_blocks(1, 1, 1), max_seq_len);
   return ws_bytes(1, head_num, head_size, n_splits(max_seq_len, st));
+}
+
+size_t orin_flash_attention_prefill_workspace_size(int32_t start_pos, int32_t seq_len,
+                                                   int32_t head_num, int32_t kv_head_num,
+                                                   int32_t head_size, int32_t dtype) {
+  if (seq_len <= 0 || start_pos < 0 || head_size <= 0 || kv_head_num <= 0 || head_num <= 0 ||
+      head_num % kv_head_num || (dtype != kF16 && dtype != kBF16))
+    return 0;
+  FwdArgs a = {};
+  a.q_tok_stride = a.o_tok_stride = (long)head_num * head_size;
+  a.q_head_stride = a.o_head_stride = a.kv_head_stride = head_size;
+  a.kv_tok_stride = (long)kv_head_num * head_size;
+  a.n_q = seq_len;
+  a.start_pos = start_pos;
+  a.Hq = head_num;
+  a.Hkv = kv_head_num;
+  a.kv_mul = head_num / kv_head_num;
+  a.head_size = head_size;
+  size_t bytes = 0;
+  (void)fwd_pp_key_split(a, dtype, device_cus(), &bytes);
+  return bytes;
 }
 
 // ------------------------------------------------------------------ batched decode

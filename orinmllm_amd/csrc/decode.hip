@@ -158,9 +158,11 @@ __device__ __forceinline__ int row_len_raw(const DecodeArgs& a, int row) {
   return a.len_base + row * a.len_step;
 }
 
-// Device-side lengths (gpu pos, context_lens) are clamped to what the launch covers.
+// A device-side length (gpu pos, context_lens) longer than the launch was sized for
+// (len_cap, from the host's max_context_len / max_seq_len) is an argument error that the
+// host cannot see.  Such a row is not attended over a truncated prefix: its output is NaN.
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int row) {
-  return min(row_len_raw(a, row), a.len_cap);
+  return row_len_raw(a, row);
 }
 
 template <typename T, int D, int G, bool PAGED>
@@ -188,6 +190,12 @@ decode_split_kernel(DecodeArgs a) {
   const int nsplit = len > 0 ? (len + a.split_tokens - 1) / a.split_tokens : 0;
 
   T* out = reinterpret_cast<T*>(a.o) + (long)row * a.o_row_stride;
+  if (len > a.len_cap) {  // longer than the launch covers: NaN output
+    if (split == 0)
+      for (int i = threadIdx.x; i < G * D; i += kDecodeThreads)
+        out[(long)(h0 + i / D) * a.o_head_stride + i % D] = from_f32<T>(__builtin_nanf(""));
+    return;
+  }
   if (len <= 0) {  // empty row: output zeros
     if (split == 0)
       for (int i = threadIdx.x; i < G * D; i += kDecodeThreads)
@@ -440,6 +448,7 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   const int h = blockIdx.x % a.Hq;
   const int row = blockIdx.x / a.Hq;
   const int len = row_len(a, row);
+  if (len > a.len_cap) return;  // the split kernel wrote NaN
   const int nsplit = len > 0 ? (len + a.split_tokens - 1) / a.split_tokens : 0;
   if (nsplit <= 1) return;
   const float* ph = a.ws + ((long)row * a.Hq + h) * a.max_splits * (D + 2);

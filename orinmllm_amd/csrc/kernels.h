@@ -23,7 +23,7 @@ struct DecodeArgs {
   const int* lens;  // len(r) = lens[r] + len_add  if lens
   int len_add;
   int len_base, len_step;  // len(r) = len_base + r*len_step otherwise
-  int len_cap;             // len(r) is clamped to len_cap (the launch was sized for it)
+  int len_cap;             // the launch covers len(r) <= len_cap; longer rows output NaN
   const int* cu_seqlens;   // varlen: rows are tokens; row r attends its segment
   int n_seg;
   void* o;  // o(r, h, j) = o[r*o_row_stride + h*o_head_stride + j]

@@ -195,11 +195,20 @@ def flash_attention_decode_fp16_gpu_pos_cu(pos_ptr, head_num, kv_head_num, head_
 flash_attention2_decode_fp16_gpu_pos_cu = flash_attention_decode_fp16_gpu_pos_cu
 
 
-def reserve_decode_workspace(head_num, head_size, max_seq_len):
-    """Allocate the library-owned flash-decode workspace now (before a graph capture)."""
+def reserve_decode_workspace(head_num, head_size, max_seq_len, stream=None, prefill_bytes=0):
+    """Allocate the library-owned flash-decode workspace of `stream` (a torch.cuda.Stream;
+    None = the current stream) now, before that stream captures a graph."""
     lib = _lib.load()
     n = lib.orin_flash_attention_decode_workspace_size(head_num, head_size, max_seq_len)
-    _lib.check("orin_attn_workspace_reserve", lib.orin_attn_workspace_reserve(n))
+    s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
+    _lib.check("orin_attn_workspace_reserve_stream",
+               lib.orin_attn_workspace_reserve_stream(n, prefill_bytes, s))
+
+
+def prefill_workspace_size(start_pos, seq_len, head_num, kv_head_num, head_size, dtype):
+    """Bytes of the library-owned key-split workspace one causal prefill launch needs."""
+    return int(_lib.load().orin_flash_attention_prefill_workspace_size(
+        start_pos, seq_len, head_num, kv_head_num, head_size, dtype))
 
 
 # ---------------------------------------------------------------- batched / paged decode

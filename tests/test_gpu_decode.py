@@ -286,7 +286,8 @@ def test_gpu_pos_decode_graph_replay(kind):
     qd = torch.zeros(head_num * d, device="cuda", dtype=TORCH[kind])
     p = torch.zeros(1, dtype=torch.int32, device="cuda")
     out = torch.zeros(head_num * d, device="cuda", dtype=TORCH[kind])
-    K.reserve_decode_workspace(head_num, d, max_seq)
+    cap = torch.cuda.Stream()
+    K.reserve_decode_workspace(head_num, d, max_seq, stream=cap)  # the capture stream's buffer
 
     def call(o):
         K.flash_attention_decode_fp16_gpu_pos_cu(p, head_num, kv_heads, d, kv_mul, layer,
@@ -299,7 +300,7 @@ def test_gpu_pos_decode_graph_replay(kind):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=cap):
         call(out)
     for pos in [4095, 5, 1000, 0, 2047]:
         q = quantize(normal(rng, head_num * d), kind)
