@@ -134,6 +134,28 @@ int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num
                                         const void* value_cache, int32_t dtype, void* stream);
 
 /*
+ * No counterpart in the reference.  For callers that cannot allocate (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc): the gpu-pos flash
+ * decode above, with its split partials in a fixed device array of
+ * orin_flash_attention_decode_noalloc_max_bytes() bytes (4 MiB) that each GPU holds
+ * until the process ends, instead of a library-owned buffer.  It allocates nothing and
+ * needs no reserve; the launch and the result equal orin_flash_attention_decode_gpu_pos
+ * bit for bit.  A launch whose partials would exceed the array (head_num * splits *
+ * (head_size + 2) * 4 bytes; at 32 heads, d 128: a cache of more than 64512 rows) returns
+ * ORIN_ERR_WORKSPACE and queues nothing.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time (other streams, concurrent graph replays) race.  Each call
+ * writes every partial it reads, so the array needs no clearing between calls.
+ */
+int orin_flash_attention_decode_gpu_pos_noalloc(const int32_t* pos_ptr, int32_t head_num,
+                                                int32_t kv_head_num, int32_t head_size,
+                                                int32_t kv_mul, int32_t layer_index,
+                                                int32_t max_seq_len, int32_t kv_dim,
+                                                const void* query, void* output,
+                                                const void* key_cache, const void* value_cache,
+                                                int32_t dtype, void* stream);
+size_t orin_flash_attention_decode_noalloc_max_bytes(void);
+
+/*
  * Library-owned workspaces (no reference counterpart: kuiper's flash decode and prefill
  * take no workspace argument).  The flash decode entry points and the key split of a
  * small causal prefill keep their partials in buffers owned by this library, one per

@@ -35,6 +35,8 @@ SIGNATURES = {
     "orin_flash_attention_prefill": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode_gpu_pos": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "orin_flash_attention_decode_gpu_pos_noalloc": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "orin_flash_attention_decode_noalloc_max_bytes": (sz, []),
     "orin_flash_attention_decode_workspace_size": (sz, [i32, i32, i32]),
     "orin_flash_attention_prefill_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "orin_attn_workspace_reserve": (C.c_int, [sz]),

@@ -404,11 +404,42 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
   return hip_status(launch_fwd_causal(a, dtype, (hipStream_t)stream));
 }
 
+// Partials of orin_flash_attention_decode_gpu_pos_noalloc: a fixed device array, so that
+// entry point never allocates.  In host code `scratch` names a host-side stand-in, not
+// device memory: its device address is looked up once per device (noalloc_scratch) and
+// only that address is passed to kernels.
+static constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_ptr;  // per device: device address of `scratch`, or null
+
+static int noalloc_scratch(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e);
+    if (!p) return ORIN_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ORIN_OK;
+}
+
+// noalloc: take the partials from the device's static scratch array instead of the
+// library-owned buffer (no allocation; ORIN_ERR_WORKSPACE if they do not fit).
 static int flash_decode_common(int32_t pos, const int32_t* pos_ptr, int32_t head_num,
                                int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
                                int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
                                const void* query, void* output, const void* key_cache,
-                               const void* value_cache, int32_t dtype, void* stream) {
+                               const void* value_cache, int32_t dtype, void* stream,
+                               bool noalloc = false) {
   if (head_size <= 0 || max_seq_len <= 0 || layer_index < 0 || kv_dim != kv_head_num * head_size)
     return ORIN_ERR_INVALID_ARG;
   if (!heads_ok(head_num, kv_head_num, kv_mul)) return ORIN_ERR_INVALID_ARG;
@@ -419,9 +450,15 @@ static int flash_decode_common(int32_t pos, const int32_t* pos_ptr, int32_t head
   DecodeArgs a = decode_defaults();
   a.split_tokens = kuiper_decode_split(head_num, kv_head_num, head_size, max_len, 0, false);
   const int splits = n_splits(max_len, a.split_tokens);
+  const size_t need = ws_bytes(1, head_num, head_size, splits);
   void* ws = nullptr;
-  int st = library_workspace(kWsDecode, (hipStream_t)stream, ws_bytes(1, head_num, head_size, splits),
-                             &ws);
+  int st;
+  if (noalloc) {
+    if (need > kNoAllocScratchBytes) return ORIN_ERR_WORKSPACE;
+    st = noalloc_scratch(&ws);
+  } else {
+    st = library_workspace(kWsDecode, (hipStream_t)stream, need, &ws);
+  }
   if (st != ORIN_OK) return st;
   const size_t layer_off = (size_t)layer_index * max_seq_len * kv_dim * elem_size(dtype);
   a.q = query;
@@ -470,6 +507,21 @@ int orin_flash_attention_decode_gpu_pos(const int32_t* pos_ptr, int32_t head_num
                              max_seq_len, kv_dim, query, output, key_cache, value_cache, dtype,
                              stream);
 }
+
+int orin_flash_attention_decode_gpu_pos_noalloc(const int32_t* pos_ptr, int32_t head_num,
+                                                int32_t kv_head_num, int32_t head_size,
+                                                int32_t kv_mul, int32_t layer_index,
+                                                int32_t max_seq_len, int32_t kv_dim,
+                                                const void* query, void* output,
+                                                const void* key_cache, const void* value_cache,
+                                                int32_t dtype, void* stream) {
+  if (!pos_ptr) return ORIN_ERR_INVALID_ARG;
+  return flash_decode_common(0, pos_ptr, head_num, kv_head_num, head_size, kv_mul, layer_index,
+                             max_seq_len, kv_dim, query, output, key_cache, value_cache, dtype,
+                             stream, true);
+}
+
+size_t orin_flash_attention_decode_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
 size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head_size,
                                                   int32_t max_seq_len) {
