@@ -303,6 +303,41 @@ def per_launch(fn, reps, warmup, stream, indexed=False):
             "min_ms": round(min(ts), 5), "max_ms": round(max(ts), 5)}
 
 
+def time_fused_pipeline(K, dtype, gen, reps=50):
+    """The C3 prefill from raw Q/K/V (Qwen3 producer + attention), two ways: the producer on
+    Q, K and V followed by the prefill, and the producer on K and V only followed by the
+    prefill with the Q producer fused into its Q load.  Median per-launch times of each
+    kernel (HIP events on the current stream) and of the pair."""
+    import torch
+    S, Hq, Hkv, d = 4096, 32, 8, 128
+    dev = "cuda"
+    q = torch.randn(S, Hq * d, device=dev, generator=gen).to(dtype)
+    k = torch.randn(S, Hkv * d, device=dev, generator=gen).to(dtype)
+    v = torch.randn(S, Hkv * d, device=dev, generator=gen).to(dtype)
+    wq = (1 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(dtype)
+    wk = (1 + 0.1 * torch.randn(d, device=dev, generator=gen)).to(dtype)
+    sn = torch.empty(S, d, device=dev)
+    cs = torch.empty(S, d, device=dev)
+    K.sin_cos_cache_calc_cu(d, S, sn, cs, 1e6)
+    kc = torch.empty(1, S, Hkv * d, device=dev, dtype=dtype)
+    vc = torch.empty_like(kc)
+    qw = torch.empty_like(q)
+    o = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    prod_qkv = lambda: K.qk_norm_rope_cu(qw, k, v, wq, wk, sn, cs, kc, vc, 0, S, 0, S, Hq, Hkv, d)
+    prod_kv = lambda: K.qk_norm_rope_cu(None, k, v, None, wk, sn, cs, kc, vc, 0, S, 0, S, Hq, Hkv, d)
+    attn = lambda: K.flash_attention_prefill_cu(0, S, Hq, Hkv, d, Hq // Hkv, 0, S, Hkv * d, qw, o,
+                                                kc, vc)
+    fused = lambda: K.flash_attention_prefill_qk_norm_rope_cu(0, S, Hq, Hkv, d, Hq // Hkv, 0, S,
+                                                              Hkv * d, q, o, kc, vc, wq, sn, cs)
+    t = {name: per_launch(fn, reps, 10, stream)["median_ms"] * 1e3
+         for name, fn in [("producer_qkv", prod_qkv), ("prefill", attn), ("producer_kv", prod_kv),
+                          ("prefill_fused_q", fused)]}
+    return {"two_pass_us": round(t["producer_qkv"] + t["prefill"], 2),
+            "fused_us": round(t["producer_kv"] + t["prefill_fused_q"], 2),
+            "kernels_us": {n: round(x, 2) for n, x in t.items()}}
+
+
 def cpu_baseline(pf, dc, min_seconds=8.0):
     """Time the oracle (all host cores, OpenMP over query rows) on the full C3 prefill and
     the full C4 decode, repeating each until it has run about min_seconds."""
@@ -476,6 +511,7 @@ def main():
     if not args.no_other_configs:
         out["other_configs"] = time_other_configs(K, gen)
     if not args.no_producers:
+        out["c3_pipeline"] = time_fused_pipeline(K, dtype, gen)
         out["producers"] = time_producers(K, make_producers(dtype, gen))
         for name, rec in out["producers"].items():
             rec["traffic"] = _bytes(traffic.get(name))

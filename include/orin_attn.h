@@ -109,6 +109,27 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
                                  const void* value_cache, int32_t dtype, void* stream);
 
 /*
+ * The Qwen3 prefill producer fused into the attention (no single reference function: it
+ * replaces, for the query, kernel::rmsnorm_kernel_cu_dim on the q heads,
+ * rmsnorm_kernel.cu:483-545, and kernel::batched_rope_kernel_cu, rope_kernel.cu:377-427,
+ * as called by kuiper/source/model/qwen3.cpp:1195-1215, and then
+ * orin_flash_attention_prefill).  `query` holds the raw rows [seq_len, dim]; each query
+ * head row i is RMS-normalised with q_norm_weight (NULL: no normalisation, the Qwen2 /
+ * Llama producer) and rotated with sin_cache/cos_cache [max_seq_len, head_size] (entry
+ * [p][2j] for the pair (j, j + head_size/2)) at position start_pos + i while the prefill
+ * loads it, with the same arithmetic as orin_qk_norm_rope: the output equals
+ * orin_qk_norm_rope on the query followed by orin_flash_attention_prefill, bit for bit, and
+ * the query buffer is left unchanged.  Keys must already be in the cache (orin_qk_norm_rope
+ * with query = NULL writes them).  fp16 / bf16, head_size 64 or 128; output must not
+ * alias query.
+ */
+int orin_flash_attention_prefill_qk_norm_rope(
+    int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t kv_head_num, int32_t head_size,
+    int32_t kv_mul, int32_t layer_index, int32_t max_seq_len, int32_t kv_dim, const void* query,
+    void* output, const void* key_cache, const void* value_cache, const void* q_norm_weight,
+    const float* sin_cache, const float* cos_cache, float eps, int32_t dtype, void* stream);
+
+/*
  * kernel::flash_attention_decode_cu / flash_attention_decode_fp16_cu /
  * flash_attention2_decode_cu / flash_attention2_decode_fp16_cu
  * (flash_attention_kernel.cuh:50-63, 84-97, 186-216).  One query row [dim] at
@@ -325,7 +346,9 @@ int orin_rope_sin_cos_cache(float* sin_cache, float* cos_cache, int32_t head_siz
  *   value_cache[layer][p][g] <- value[t, g]
  * rmsnorm(x) = x / sqrt(mean(x^2) + eps) in fp32; rope rotates pairs (j, j + d/2) with
  * sin_cache/cos_cache[p][2j].  A NULL weight skips that normalisation (Qwen2 / Llama).
- * head_size 128 or 256; fp32 / fp16 / bf16 (weights in the same type).
+ * query may be NULL: only the key and value rows are produced (for
+ * orin_flash_attention_prefill_qk_norm_rope, which applies the query part itself).
+ * head_size 64, 128 or 256; fp32 / fp16 / bf16 (weights in the same type).
  */
 int orin_qk_norm_rope(void* query, const void* key, const void* value,
                       const void* q_norm_weight, const void* k_norm_weight,

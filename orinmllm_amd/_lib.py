@@ -33,6 +33,7 @@ SIGNATURES = {
     "orin_mha_kernel_gpu_pos": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp]),
     "orin_batched_mha": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp]),
     "orin_flash_attention_prefill": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "orin_flash_attention_prefill_qk_norm_rope": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, f32, i32, vp]),
     "orin_flash_attention_decode": (C.c_int, [i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode_gpu_pos": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "orin_flash_attention_decode_gpu_pos_noalloc": (C.c_int, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),

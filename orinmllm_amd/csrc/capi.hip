@@ -353,11 +353,13 @@ int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32
 
 static size_t elem_size(int dtype) { return dtype == kF32 ? 4 : 2; }
 
-int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
-                                 int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
-                                 int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
-                                 const void* query, void* output, const void* key_cache,
-                                 const void* value_cache, int32_t dtype, void* stream) {
+static int prefill_common(int32_t start_pos, int32_t seq_len, int32_t head_num,
+                          int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                          int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                          const void* query, void* output, const void* key_cache,
+                          const void* value_cache, int32_t dtype, void* stream,
+                          const void* q_norm_weight, const float* rope_sin,
+                          const float* rope_cos, float eps) {
   if (head_size <= 0 || seq_len <= 0 || max_seq_len <= 0 || start_pos < 0 || layer_index < 0 ||
       kv_dim != kv_head_num * head_size || start_pos + seq_len > max_seq_len)
     return ORIN_ERR_INVALID_ARG;
@@ -367,8 +369,9 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
   const size_t layer_off = (size_t)layer_index * max_seq_len * kv_dim * elem_size(dtype);
   const char* k = static_cast<const char*>(key_cache) + layer_off;
   const char* v = static_cast<const char*>(value_cache) + layer_off;
+  const bool fused = rope_sin != nullptr;
   if (dtype == kF32) {
-    if (!decode_supports(kF32, head_size)) return ORIN_ERR_UNSUPPORTED;
+    if (fused || !decode_supports(kF32, head_size)) return ORIN_ERR_UNSUPPORTED;
     return prefill_rows(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, query,
                         output, k, v, kv_dim, kF32, (hipStream_t)stream);
   }
@@ -391,6 +394,17 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
   a.kv_mul = kv_mul;
   a.head_size = head_size;
   a.scale_log2 = resolve_scale(0.f, head_size) * kLog2e;
+  if (fused) {
+    // The fused Q producer runs in the ping-pong kernel's Q load (head sizes 64 and 128);
+    // it reads the raw query while other rows' outputs are written, so no aliasing.
+    if ((head_size != 64 && head_size != 128) || !fwd_pp_supports(a, dtype))
+      return ORIN_ERR_UNSUPPORTED;
+    if (query == output || !rope_cos || !(eps >= 0.f)) return ORIN_ERR_INVALID_ARG;
+    a.q_norm_weight = q_norm_weight;
+    a.rope_sin = rope_sin;
+    a.rope_cos = rope_cos;
+    a.eps = eps;
+  }
   // Too few query blocks to fill the device: split their keys (library workspace).
   size_t split_bytes = 0;
   const int chunk = fwd_pp_key_split(a, dtype, device_cus(), &split_bytes);
@@ -402,6 +416,27 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
     a.ws = static_cast<float*>(ws);
   }
   return hip_status(launch_fwd_causal(a, dtype, (hipStream_t)stream));
+}
+
+int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
+                                 int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
+                                 int32_t layer_index, int32_t max_seq_len, int32_t kv_dim,
+                                 const void* query, void* output, const void* key_cache,
+                                 const void* value_cache, int32_t dtype, void* stream) {
+  return prefill_common(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul,
+                        layer_index, max_seq_len, kv_dim, query, output, key_cache, value_cache,
+                        dtype, stream, nullptr, nullptr, nullptr, 0.f);
+}
+
+int orin_flash_attention_prefill_qk_norm_rope(
+    int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t kv_head_num, int32_t head_size,
+    int32_t kv_mul, int32_t layer_index, int32_t max_seq_len, int32_t kv_dim, const void* query,
+    void* output, const void* key_cache, const void* value_cache, const void* q_norm_weight,
+    const float* sin_cache, const float* cos_cache, float eps, int32_t dtype, void* stream) {
+  if (!sin_cache || !cos_cache) return ORIN_ERR_INVALID_ARG;
+  return prefill_common(start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul,
+                        layer_index, max_seq_len, kv_dim, query, output, key_cache, value_cache,
+                        dtype, stream, q_norm_weight, sin_cache, cos_cache, eps);
 }
 
 // Partials of orin_flash_attention_decode_gpu_pos_noalloc: a fixed device array, so that
@@ -822,7 +857,7 @@ int orin_qk_norm_rope(void* query, const void* key, const void* value,
                       int32_t start_pos, const int32_t* pos_ptr, int32_t seq_len,
                       int32_t head_num, int32_t kv_head_num, int32_t head_size, float eps,
                       int32_t dtype, void* stream) {
-  if (!query || !key || !value || !sin_cache || !cos_cache || !key_cache || !value_cache)
+  if (!key || !value || !sin_cache || !cos_cache || !key_cache || !value_cache)
     return ORIN_ERR_INVALID_ARG;
   if (seq_len <= 0 || head_num <= 0 || kv_head_num <= 0 || head_size <= 0 || layer_index < 0 ||
       max_seq_len <= 0 || start_pos < 0 || !(eps >= 0.f))

@@ -39,6 +39,46 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
 // Hardware base-2 exponential (v_exp_f32).  exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---------------------------------------------------------------- Q/K producer arithmetic
+// Shared by the Q/K producer (producers.hip, qk_norm_rope_kernel) and the prefill's fused
+// Q load (fwd_pp.hip), so that both produce the same bits for the same row.
+// Sum of squares of one 8-element chunk pair: elements lo[i] (first half of the head) and
+// hi[i] (second half), nested as fma(lo, lo, fma(hi, hi, acc)) from i = 0.
+__device__ __forceinline__ float qk_chunk_sumsq(const float* lo, const float* hi) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
+  return ss;
+}
+// Row sum of the chunk sums c[0 .. N) in the order of an xor butterfly over N lanes
+// (strides 1, 2, 4, ...): every lane of such a butterfly ends with this value.
+template <int N>
+__device__ __forceinline__ float qk_butterfly_sum(const float (&c)[N]) {
+  float v[N];
+#pragma unroll
+  for (int l = 0; l < N; ++l) v[l] = c[l];
+#pragma unroll
+  for (int m = 1; m < N; m <<= 1) {
+    float w[N];
+#pragma unroll
+    for (int l = 0; l < N; ++l) w[l] = v[l] + v[l ^ m];
+#pragma unroll
+    for (int l = 0; l < N; ++l) v[l] = w[l];
+  }
+  return v[0];
+}
+// 1 / rms of a head row: 1 / sqrt(sum(x^2) / d + eps) (rmsnorm_kernel.cu:483-545).
+__device__ __forceinline__ float qk_rms_inv(float ss, int d, float eps) {
+  return 1.0f / sqrtf(ss / (float)d + eps);
+}
+// Rotate-half RoPE of the pair (x_j, x_{j+d/2}) by the angle with cosine cv and sine sv
+// (rope_kernel.cu:464-509).
+__device__ __forceinline__ void qk_rope(float lo, float hi, float cv, float sv, float& ro,
+                                        float& rh) {
+  ro = __builtin_fmaf(cv, lo, -(sv * hi));
+  rh = __builtin_fmaf(cv, hi, sv * lo);
+}
+
 // ---------------------------------------------------------------- 16-byte lane chunk
 // A lane chunk is 16 bytes of one K or V row: 8 halves or 4 floats.
 template <typename T>

@@ -483,7 +483,7 @@ bool use_pp(const FwdArgs& a, int dtype) {
     return -1;
   }();
   if (mode == 0 || !fwd_pp_supports(a, dtype)) return false;
-  if (mode == 1 || (CAUSAL && a.key_chunk_tiles > 0)) return true;
+  if (mode == 1 || (CAUSAL && (a.key_chunk_tiles > 0 || a.rope_sin))) return true;
   const long blocks = CAUSAL ? (long)((a.n_q + 255) / 256) * a.Hq
                              : (long)a.n_seg * ((a.max_seqlen + 255) / 256) * a.Hq;
   return blocks >= 256;

@@ -33,7 +33,7 @@
 // Key split.  A causal launch with fewer 256-query blocks than CUs is bounded by its
 // longest block; the host then cuts each block's keys before its diagonal into chunks
 // (key_chunk_tiles), each run by its own workgroup, and fwd_pp_merge combines the
-// chunks' partials (O / l in the input type, fp32 m and l) in a second launch.
+// chunks' fp32 partials (unnormalised O, m and l) in a second launch.
 #include "common.h"
 #include "kernels.h"
 
@@ -187,10 +187,10 @@ __host__ __device__ inline int pp_items(const FwdArgs& a, int C) {
   for (int b = 0; b < nqb; ++b) n += pp_block_chunks(a, b, C);
   return n;
 }
-// Workspace of a key split: O rows [items * Hq * PBM][head_size] in the 16-bit input
-// type, then (m, l) [items * Hq * PBM][2] fp32.  Offsets in floats.
+// Workspace of a key split: unnormalised O rows [items * Hq * PBM][head_size] fp32, then
+// (m, l) [items * Hq * PBM][2] fp32.  Offsets in floats.
 __host__ __device__ inline long pp_ml_offset(const FwdArgs& a, int D) {
-  return (long)pp_items(a, a.key_chunk_tiles) * a.Hq * PBM * D / 2;
+  return (long)pp_items(a, a.key_chunk_tiles) * a.Hq * PBM * D;
 }
 
 // Order of the MFMAs of one phase: QK steps (2 per 16-wide slice of the head) and PV steps
@@ -230,6 +230,70 @@ __device__ __forceinline__ void sgb_head() {
     constexpr PhaseOrder<NQK, NPV> o{};
     __builtin_amdgcn_sched_group_barrier(0x100, o.is_qk[I] ? 1 : 2, 0);
     sgb_head<NQK, NPV, I + 1>();
+  }
+}
+
+// Fused Q producer on the Q fragments of one lane: qf[s] holds elements 16s + 8hf .. +7 of
+// the lane's query row, so chunk c = 2s + hf (elements 8c .. 8c+7) of the first half of the
+// head and its rotation partner (elements d/2 + 8c ..) are in qf[s] and qf[s + QS/2]; the
+// partner lane (lane ^ 32) holds the other chunks.  Same arithmetic as qk_norm_rope_kernel
+// (producers.hip), so the rounded row equals the one that producer writes.
+template <typename T, int D>
+__device__ __forceinline__ void fuse_q_producer(const FwdArgs& a, u32x4 (&qf)[(D + 15) / 16],
+                                                bool live, int pos, int hf) {
+  constexpr int QS = D / 16, H2 = QS / 2;  // chunks per lane in each half
+  float lo[H2][8], hi[H2][8], cs[2 * H2];
+  float own[H2];
+#pragma unroll
+  for (int s = 0; s < H2; ++s) {
+    chunk_unpack(Chunk<T>{qf[s]}, lo[s]);
+    chunk_unpack(Chunk<T>{qf[s + H2]}, hi[s]);
+    own[s] = qk_chunk_sumsq(lo[s], hi[s]);
+  }
+#pragma unroll
+  for (int s = 0; s < H2; ++s) {
+    const float other = partner32(own[s]);
+    cs[2 * s + hf] = own[s];
+    cs[2 * s + (hf ^ 1)] = other;
+  }
+  if (!live) return;  // rows past the end stay zero
+  if (a.q_norm_weight) {
+    const float inv = qk_rms_inv(qk_butterfly_sum(cs), D, a.eps);
+    const T* w = reinterpret_cast<const T*>(a.q_norm_weight);
+#pragma unroll
+    for (int s = 0; s < H2; ++s) {
+      float wl[8], wh[8];
+      chunk_unpack(load_chunk(w + 16 * s + 8 * hf), wl);
+      chunk_unpack(load_chunk(w + D / 2 + 16 * s + 8 * hf), wh);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        lo[s][i] = lo[s][i] * inv * wl[i];
+        hi[s][i] = hi[s][i] * inv * wh[i];
+      }
+    }
+  }
+  // table entries [pos][2j], j = 16s + 8hf + i
+  const float* sn = a.rope_sin + (long)pos * D;
+  const float* cn = a.rope_cos + (long)pos * D;
+  typedef T T8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int s = 0; s < H2; ++s) {
+    T8 rl, rh;
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + 32 * s + 16 * hf + 4 * c4);
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(cn + 32 * s + 16 * hf + 4 * c4);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = 2 * c4 + e;
+        float ro, rv;
+        qk_rope(lo[s][i], hi[s][i], k4[2 * e], s4[2 * e], ro, rv);
+        rl[i] = from_f32<T>(ro);
+        rh[i] = from_f32<T>(rv);
+      }
+    }
+    qf[s] = __builtin_bit_cast(u32x4, rl);
+    qf[s + H2] = __builtin_bit_cast(u32x4, rh);
   }
 }
 
@@ -391,6 +455,9 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       u32x4 val = {0u, 0u, 0u, 0u};  // rows past the end and the zero padding of the head
       if (qi < q_n && 16 * s + 8 * hf < D) val = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * hf);
       qf[s] = val;
+    }
+    if constexpr (CAUSAL && (D == 64 || D == 128)) {
+      if (a.rope_sin) fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, hf);
     }
   }
 
@@ -611,21 +678,18 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // ------------------------------------------------------------ normalise and store
   const float l_tot = l_run + partner32(l_run);
   if (partial) {
-    // Partial of this key chunk per query row: O / l rounded to T (as an output row), and
-    // (m, l) in fp32 after all items' O rows.
+    // Partial of this key chunk per query row: unnormalised O and (m, l), fp32.
     const long row = (long)blockIdx.x * PBM + (qi - q_lo);
     if (qi < q_n) {
-      const float inv = 1.f / l_tot;
-      T* pr = reinterpret_cast<T*>(a.ws) + row * D;
+      float* pr = a.ws + row * D;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
           const int d0 = t * 32 + 8 * rg + 4 * hf;
           if (d0 >= D) continue;
-          u32x2 pk = {pack2<T>(oacc[t][4 * rg] * inv, oacc[t][4 * rg + 1] * inv),
-                      pack2<T>(oacc[t][4 * rg + 2] * inv, oacc[t][4 * rg + 3] * inv)};
-          *reinterpret_cast<u32x2*>(pr + d0) = pk;
+          *reinterpret_cast<f32x4*>(pr + d0) =
+              f32x4{oacc[t][4 * rg], oacc[t][4 * rg + 1], oacc[t][4 * rg + 2], oacc[t][4 * rg + 3]};
         }
       if (hf == 0) {
         float* ml = a.ws + pp_ml_offset(a, D) + row * 2;
@@ -652,74 +716,61 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 }
 
-// Merge the key-chunk partials of the split query blocks, O = sum_c w_c O_c / sum_c w_c
-// with w_c = 2^(m_c - M) l_c.  Workgroup (head, query block, 64-row quarter) gives each
-// row ceil(D/32) neighbouring threads, thread p of a row covering dimensions
-// [32p, 32p + 32); every load a thread needs (the chunks' (m, l) and 64-byte row pieces)
-// is issued before any is used.
+// Merge the key-chunk partials of the split query blocks:
+// O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  A thread owns 8 dimensions of one row
+// (16 rows per workgroup, a row's threads neighbours so a wave reads whole rows); every
+// load it needs is issued before any is used.
 constexpr int kMergeMaxChunks = 8;
+constexpr int kMergeRows = 16;
 template <typename T, int D>
-__global__ void __launch_bounds__(PBM) fwd_pp_merge(FwdArgs a) {
-  constexpr int NP = (D + 31) / 32;  // 32-dimension parts of a row
+__global__ void __launch_bounds__(kMergeRows * ((D + 7) / 8)) fwd_pp_merge(FwdArgs a) {
+  constexpr int NP = (D + 7) / 8;  // 8-dimension parts of a row
   const int C = a.key_chunk_tiles;
-  // Workgroup: 64 rows of one (block, head), NP neighbouring threads per row, so a wave's
-  // loads cover whole rows.
-  const int quarter = (int)blockIdx.x % (PBM / 64);
-  const int hb = (int)blockIdx.x / (PBM / 64);
+  const int sub = (int)blockIdx.x % (PBM / kMergeRows);
+  const int hb = (int)blockIdx.x / (PBM / kMergeRows);
   const int head = hb % a.Hq, qb = hb / a.Hq;
   const int n_ch = pp_block_chunks(a, qb, C);
   if (n_ch <= 1) return;
   const int part = (int)threadIdx.x % NP;
-  const int r = quarter * 64 + (int)threadIdx.x / NP;
+  const int r = sub * kMergeRows + (int)threadIdx.x / NP;
   const int qi = qb * PBM + r;
   if (qi >= a.n_q) return;
   const int nqb = (a.n_q + PBM - 1) / PBM;
   int item0 = 0;  // the items of blocks qb+1 .. nqb-1 come first
   for (int b = nqb - 1; b > qb; --b) item0 += pp_block_chunks(a, b, C);
   const float* ml = a.ws + pp_ml_offset(a, D);
-  const T* po = reinterpret_cast<const T*>(a.ws);
-  const int d0 = 32 * part;
-  constexpr int NQ = 4;  // 16-byte pieces per part
+  const int d0 = 8 * part;
   float m[kMergeMaxChunks], l[kMergeMaxChunks];
-  Chunk<T> x[kMergeMaxChunks][NQ];
+  f32x4 x[kMergeMaxChunks][2];
 #pragma unroll
   for (int c = 0; c < kMergeMaxChunks; ++c) {
     const long row = ((long)(item0 + min(c, n_ch - 1)) * a.Hq + head) * PBM + r;
     m[c] = c < n_ch ? ml[row * 2] : -INFINITY;
     l[c] = c < n_ch ? ml[row * 2 + 1] : 0.f;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const int d = d0 + 8 * j;
-      if (c < n_ch && d < D) x[c][j] = load_chunk(po + row * D + d);
-      else x[c][j].raw = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < 2; ++j)
+      x[c][j] = (c < n_ch && d0 + 4 * j < D) ? *reinterpret_cast<const f32x4*>(a.ws + row * D + d0 + 4 * j)
+                                             : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float M = m[0];
 #pragma unroll
   for (int c = 1; c < kMergeMaxChunks; ++c) M = fmaxf(M, m[c]);
-  float W = 0.f, o[32];
+  float W = 0.f, o[8];
 #pragma unroll
-  for (int e = 0; e < 32; ++e) o[e] = 0.f;
+  for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
   for (int c = 0; c < kMergeMaxChunks; ++c) {
-    const float w = c < n_ch ? fast_exp2(m[c] - M) * l[c] : 0.f;
-    W += w;
+    const float w = c < n_ch ? fast_exp2(m[c] - M) : 0.f;
+    W = __builtin_fmaf(w, l[c], W);
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      typedef T T8 __attribute__((ext_vector_type(8)));
-      const T8 v = __builtin_bit_cast(T8, x[c][j].raw);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[8 * j + e] = __builtin_fmaf(w, (float)v[e], o[8 * j + e]);
-    }
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(w, x[c][e >> 2][e & 3], o[e]);
   }
   const float inv = 1.f / W;
+  if (d0 >= D) return;
   T* op = reinterpret_cast<T*>(a.o) + (long)qi * a.o_tok_stride + (long)head * a.o_head_stride;
-#pragma unroll
-  for (int e = 0; e < 32; e += 4) {
-    if (d0 + e >= D) break;
-    u32x2 pk = {pack2<T>(o[e] * inv, o[e + 1] * inv), pack2<T>(o[e + 2] * inv, o[e + 3] * inv)};
-    *reinterpret_cast<u32x2*>(op + d0 + e) = pk;
-  }
+  u32x4 pk = {pack2<T>(o[0] * inv, o[1] * inv), pack2<T>(o[2] * inv, o[3] * inv),
+              pack2<T>(o[4] * inv, o[5] * inv), pack2<T>(o[6] * inv, o[7] * inv)};
+  *reinterpret_cast<u32x4*>(op + d0) = pk;
 }
 
 template <typename T, bool CAUSAL, int D>
@@ -743,8 +794,8 @@ hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
                      PLDS_BYTES, stream, a);
   if (CAUSAL && a.key_chunk_tiles > 0) {
     const int nqb = (a.n_q + PBM - 1) / PBM;
-    hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * (PBM / 64))),
-                       dim3(64 * ((D + 31) / 32)), 0, stream, a);
+    hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * (PBM / kMergeRows))),
+                       dim3(kMergeRows * ((D + 7) / 8)), 0, stream, a);
   }
   return hipGetLastError();
 }
@@ -787,7 +838,7 @@ int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
     const int diag_extra = longest - pp_block_diag(a, nqb - 1);
     if (3 * (C + diag_extra) > 2 * longest) return 0;
     const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
-    *ws_bytes = rows * a.head_size * 2 + rows * 2 * sizeof(float);
+    *ws_bytes = rows * a.head_size * sizeof(float) + rows * 2 * sizeof(float);
     return C;
   }
   return 0;

@@ -56,10 +56,19 @@ struct FwdArgs {
   float scale_log2;
   // Causal key split (fwd_pp.hip): > 0 cuts each query block's keys before its diagonal
   // into chunks of this many 64-key tiles (the diagonal tiles join the last chunk); the
-  // chunks of a block write partials to ws (normalised O rows in the input type, then
-  // fp32 (m, l)) and a second launch merges them.  0 = off.
+  // chunks of a block write fp32 partials to ws (unnormalised O rows, then (m, l)) and a
+  // second launch merges them.  0 = off.
   int key_chunk_tiles;
   float* ws;
+  // Fused Q producer (fwd_pp.hip, causal, head sizes 64 / 128): q holds the raw query rows;
+  // row i is RMS-normalised (when q_norm_weight is non-null, with eps) and rotated with the
+  // rope_sin / rope_cos tables (entry [p][2j] for pair (j, j + d/2)) at position
+  // start_pos + i as it is loaded, with the arithmetic of launch_qk_norm_rope.  Null rope
+  // tables = off.
+  const void* q_norm_weight;
+  const float* rope_sin;
+  const float* rope_cos;
+  float eps;
 };
 
 bool fwd_supports(int dtype, int head_size);

@@ -173,12 +173,14 @@ __global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs
   const int lane = threadIdx.x & 63;
   const int l = lane % LPU;
   const long unit = ((long)blockIdx.x * kProdThreads + threadIdx.x) / LPU;
-  const int units = a.Hq + a.Hkv;
+  // Units per token: the Hq query heads (unless q is null: K/V only), then the Hkv key heads.
+  const int nq = a.q ? a.Hq : 0;
+  const int units = nq + a.Hkv;
   const int t = (int)(unit / units);
   const bool live = t < a.seq_len;
   const int u = (int)(unit % units);
-  const bool is_q = u < a.Hq;
-  const int h = is_q ? u : u - a.Hq;
+  const bool is_q = u < nq;
+  const int h = is_q ? u : u - nq;
   const int start = a.pos_ptr ? *a.pos_ptr : a.start_pos;
   const int pos = start + (live ? t : 0);
 
@@ -189,8 +191,12 @@ __global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs
   if (live) {
     unpack16<T>(*reinterpret_cast<const u32x4*>(x + VEC * l), lo);
     unpack16<T>(*reinterpret_cast<const u32x4*>(x + D / 2 + VEC * l), hi);
+    if constexpr (VEC == 8) {
+      ss = qk_chunk_sumsq(lo, hi);
+    } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
+      for (int i = 0; i < VEC; ++i) ss = __builtin_fmaf(lo[i], lo[i], __builtin_fmaf(hi[i], hi[i], ss));
+    }
   }
   // sum over the unit's LPU lanes (aligned groups; every lane runs the shuffles)
 #pragma unroll
@@ -198,7 +204,7 @@ __global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs
   if (!live) return;
   const T* w = reinterpret_cast<const T*>(is_q ? a.q_weight : a.k_weight);
   if (w) {
-    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    const float inv = qk_rms_inv(ss, D, a.eps);
     float wl[VEC], wh[VEC];
     unpack16<T>(*reinterpret_cast<const u32x4*>(w + VEC * l), wl);
     unpack16<T>(*reinterpret_cast<const u32x4*>(w + D / 2 + VEC * l), wh);
@@ -220,8 +226,7 @@ __global__ void __launch_bounds__(kProdThreads) qk_norm_rope_kernel(NormRopeArgs
     for (int e = 0; e < 2; ++e) {
       const int i = 2 * c4 + e;
       const float sv = s4[2 * e], cv = k4[2 * e];
-      ro[i] = cv * lo[i] - sv * hi[i];
-      rh[i] = cv * hi[i] + sv * lo[i];
+      qk_rope(lo[i], hi[i], cv, sv, ro[i], rh[i]);
     }
   }
   T* out = is_q ? reinterpret_cast<T*>(a.q) + ((long)t * a.Hq + h) * D
@@ -410,7 +415,7 @@ hipError_t launch_kv_convert(void* contig, void* pool, const int* block_table,
 
 bool norm_rope_supports(int dtype, int head_size) {
   return (dtype == kF32 || dtype == kF16 || dtype == kBF16) &&
-         (head_size == 128 || head_size == 256);
+         (head_size == 64 || head_size == 128 || head_size == 256);
 }
 
 hipError_t launch_qk_norm_rope(void* q, const void* k, const void* v, const void* q_weight,
@@ -421,13 +426,16 @@ hipError_t launch_qk_norm_rope(void* q, const void* k, const void* v, const void
                                hipStream_t stream) {
   NormRopeArgs a{q, k, v, q_weight, k_weight, sin_cache, cos_cache, k_cache, v_cache,
                  cache_tok_stride, pos_ptr, start_pos, seq_len, Hq, Hkv, head_size, eps};
-  const long units = (long)seq_len * (Hq + Hkv);
+  const long units = (long)seq_len * ((q ? Hq : 0) + Hkv);
   if (units <= 0) return hipSuccess;
   return by_dtype(dtype, [&](auto z) {
     using T = decltype(z);
     const long lpu = head_size / 2 / (16 / (long)sizeof(T));
     const unsigned grid = grid_for(units * lpu);
-    if (head_size == 128)
+    if (head_size == 64)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<T, 64>), dim3(grid), dim3(kProdThreads), 0, stream,
+                         a);
+    else if (head_size == 128)
       hipLaunchKernelGGL((qk_norm_rope_kernel<T, 128>), dim3(grid), dim3(kProdThreads), 0, stream,
                          a);
     else

@@ -162,6 +162,27 @@ flash_attention2_prefill_cu = flash_attention_prefill_cu
 flash_attention2_prefill_fp16_cu = flash_attention_prefill_cu
 
 
+def flash_attention_prefill_qk_norm_rope_cu(start_pos, seq_len, head_num, kv_head_num,
+                                            head_size, kv_mul, layer_index, max_seq_len, kv_dim,
+                                            query, output, key_cache, value_cache,
+                                            q_norm_weight, sin_cache, cos_cache, eps=1e-6,
+                                            config=None):
+    """Causal prefill whose query rows are RMS-normalised (q_norm_weight, may be None) and
+    rotated (sin/cos caches) as they are loaded; equals qk_norm_rope_cu on the query then
+    flash_attention_prefill_cu, bit for bit.  query is left unchanged."""
+    dt = _dtype(query, output, key_cache, value_cache,
+                *[w for w in (q_norm_weight,) if w is not None])
+    if sin_cache.dtype != torch.float32 or cos_cache.dtype != torch.float32:
+        raise ValueError("sin/cos caches are fp32")
+    _lib.check("orin_flash_attention_prefill_qk_norm_rope",
+               _lib.load().orin_flash_attention_prefill_qk_norm_rope(
+                   start_pos, seq_len, head_num, kv_head_num, head_size, kv_mul, layer_index,
+                   max_seq_len, kv_dim, _ptr(query, "query"), _ptr(output, "output"),
+                   _ptr(key_cache, "key_cache"), _ptr(value_cache, "value_cache"),
+                   _ptr(q_norm_weight, "q_norm_weight"), _ptr(sin_cache, "sin_cache"),
+                   _ptr(cos_cache, "cos_cache"), float(eps), dt, _stream(config)))
+
+
 def flash_attention_decode_cu(pos, head_num, kv_head_num, head_size, kv_mul, layer_index,
                               max_seq_len, kv_dim, query, output, key_cache, value_cache,
                               config=None):
@@ -378,7 +399,7 @@ def qk_norm_rope_cu(query, key, value, q_norm_weight, k_norm_weight, sin_cache, 
     key and value rows stored at positions start_pos.. of layer layer_index of the kuiper
     caches.  q/k_norm_weight may be None (no normalisation).  pos_ptr (int32 GPU tensor)
     replaces start_pos when given."""
-    dt = _dtype(query, key, value, key_cache, value_cache,
+    dt = _dtype(*[x for x in (query,) if x is not None], key, value, key_cache, value_cache,
                 *[w for w in (q_norm_weight, k_norm_weight) if w is not None])
     _lib.check("orin_qk_norm_rope", _lib.load().orin_qk_norm_rope(
         _ptr(query, "query"), _ptr(key, "key"), _ptr(value, "value"),
