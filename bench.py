@@ -330,12 +330,17 @@ def time_fused_pipeline(K, dtype, gen, reps=50):
                                                 kc, vc)
     fused = lambda: K.flash_attention_prefill_qk_norm_rope_cu(0, S, Hq, Hkv, d, Hq // Hkv, 0, S,
                                                               Hkv * d, q, o, kc, vc, wq, sn, cs)
+    wo = (torch.randn(Hq * d, Hq * d, device=dev, generator=gen) / (Hq * d) ** 0.5).to(dtype)
+    y = torch.empty_like(q)
+    proj = lambda: K.batched_matmul_kernel_cu(o, wo, y, S)
     t = {name: per_launch(fn, reps, 10, stream)["median_ms"] * 1e3
          for name, fn in [("producer_qkv", prod_qkv), ("prefill", attn), ("producer_kv", prod_kv),
-                          ("prefill_fused_q", fused)]}
+                          ("prefill_fused_q", fused), ("wo_projection", proj)]}
+    wo_tflops = 2.0 * S * (Hq * d) ** 2 / (t["wo_projection"] * 1e-6) / 1e12
     return {"two_pass_us": round(t["producer_qkv"] + t["prefill"], 2),
             "fused_us": round(t["producer_kv"] + t["prefill_fused_q"], 2),
-            "kernels_us": {n: round(x, 2) for n, x in t.items()}}
+            "kernels_us": {n: round(x, 2) for n, x in t.items()},
+            "wo_projection_TFLOP/s": round(wo_tflops, 1)}
 
 
 def cpu_baseline(pf, dc, min_seconds=8.0):

@@ -285,6 +285,23 @@ int orin_vision_attention_varlen(const void* q, const void* k, const void* v, vo
                                  int32_t num_tokens, int32_t num_heads, int32_t head_dim,
                                  float softmax_scale, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------ output projection */
+
+/*
+ * kernel::batched_matmul_kernel_cu / batched_matmul_kernel_cu_pure_fp16
+ * (kuiper/source/op/kernels/cuda/matmul_kernel.cuh:15-41), as the prefill runs the wo
+ * projection on the attention output (kuiper/source/model/qwen_base.cpp:464-474):
+ *   output[b, k] = scale * sum_m input[b, m] * weight[k, m]
+ * input [batch_size, in_dim] (the attention output [tokens, head_num*head_size], as the
+ * attention entry points store it), weight [out_dim, in_dim], output [batch_size, out_dim],
+ * all row-major in `dtype` (fp32 / fp16 / bf16); fp32 accumulation.  A plain GEMM, run by
+ * rocBLAS on `stream`.  The first call on a device creates its rocBLAS handle (not under
+ * graph capture).
+ */
+int orin_batched_matmul(const void* input, const void* weight, void* output, int32_t batch_size,
+                        int32_t in_dim, int32_t out_dim, float scale, int32_t dtype,
+                        void* stream);
+
 /* ------------------------------------------------------------------ KV-cache writes */
 
 /*

@@ -49,6 +49,7 @@ SIGNATURES = {
     "orin_attn_decode_paged": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, i32, i32, vp, i32, i32, f32, i32, vp, sz, vp]),
     "orin_vision_attention_pretransposed": (C.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, f32, i32, vp]),
     "orin_vision_attention_varlen": (C.c_int, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]),
+    "orin_batched_matmul": (C.c_int, [vp, vp, vp, i32, i32, i32, f32, i32, vp]),
     "orin_copy_to_kv_cache": (C.c_int, [vp, vp, vp, i32, i32, i32, i32, vp]),
     "orin_kv_cache_write_paged": (C.c_int, [vp, vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
     "orin_kv_cache_convert": (C.c_int, [vp, i64, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]),

@@ -18,7 +18,7 @@ REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborin_attn.so")
-SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "capi.hip"]
+SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "outproj.hip", "capi.hip"]
 # C++ host mirror of kuiper's kernel:: functions and op:: layers over the C ABI.
 HOST_DIR = os.path.join(PKG_DIR, "cpp")
 HOST_SOURCES = ["base.cpp", "kernels.cpp", "layers.cpp"]
@@ -85,7 +85,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # rocBLAS serves the output projection (a plain GEMM); everything else is this library's.
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -783,6 +783,24 @@ int orin_vision_attention_varlen(const void* q, const void* k, const void* v, vo
 }
 
 
+// ------------------------------------------------------------------ output projection
+
+int orin_batched_matmul(const void* input, const void* weight, void* output, int32_t batch_size,
+                        int32_t in_dim, int32_t out_dim, float scale, int32_t dtype,
+                        void* stream) {
+  if (!input || !weight || !output || batch_size <= 0 || in_dim <= 0 || out_dim <= 0)
+    return ORIN_ERR_INVALID_ARG;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return ORIN_ERR_UNSUPPORTED;
+  const int st = output_projection(input, weight, output, batch_size, in_dim, out_dim, scale,
+                                   dtype, (hipStream_t)stream);
+  if (st == -2) return ORIN_ERR_UNSUPPORTED;
+  if (st != 0) {
+    g_last_hip_error = "rocBLAS gemm_ex failed";
+    return ORIN_ERR_LAUNCH;
+  }
+  return ORIN_OK;
+}
+
 // ------------------------------------------------------------------ KV-cache writes
 
 static bool dtype_ok(int32_t dtype) {

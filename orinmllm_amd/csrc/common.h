@@ -77,6 +77,10 @@ __device__ __forceinline__ void qk_rope(float lo, float hi, float cv, float sv, 
                                         float& rh) {
   ro = __builtin_fmaf(cv, lo, -(sv * hi));
   rh = __builtin_fmaf(cv, hi, sv * lo);
+  // Both results are fp32 values here: the empty asm keeps the compiler from fusing the fma
+  // with a later conversion to 16 bits (v_fma_mix*_f16 rounds once, fma then convert twice),
+  // a choice it makes per call site, so every kernel using this rounds alike.
+  __asm__("" : "+v"(ro), "+v"(rh));
 }
 
 // ---------------------------------------------------------------- 16-byte lane chunk

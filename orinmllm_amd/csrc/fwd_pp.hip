@@ -237,11 +237,34 @@ __device__ __forceinline__ void sgb_head() {
 // the lane's query row, so chunk c = 2s + hf (elements 8c .. 8c+7) of the first half of the
 // head and its rotation partner (elements d/2 + 8c ..) are in qf[s] and qf[s + QS/2]; the
 // partner lane (lane ^ 32) holds the other chunks.  Same arithmetic as qk_norm_rope_kernel
-// (producers.hip), so the rounded row equals the one that producer writes.
+// (producers.hip), so the rounded row equals the one that producer writes.  The weight and
+// table loads do not depend on the row and are issued first (rows past the end read the
+// tables at position pos_ok and are left unchanged).
 template <typename T, int D>
 __device__ __forceinline__ void fuse_q_producer(const FwdArgs& a, u32x4 (&qf)[(D + 15) / 16],
-                                                bool live, int pos, int hf) {
+                                                bool live, int pos, int pos_ok, int hf) {
   constexpr int QS = D / 16, H2 = QS / 2;  // chunks per lane in each half
+  const int p = live ? pos : pos_ok;
+  // table entries [p][2j], j = 16s + 8hf + i: four 16-byte loads per table and chunk
+  const float* sn = a.rope_sin + (long)p * D + 16 * hf;
+  const float* cn = a.rope_cos + (long)p * D + 16 * hf;
+  f32x4 s4[H2][4], k4[H2][4];
+#pragma unroll
+  for (int s = 0; s < H2; ++s)
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      s4[s][c4] = *reinterpret_cast<const f32x4*>(sn + 32 * s + 4 * c4);
+      k4[s][c4] = *reinterpret_cast<const f32x4*>(cn + 32 * s + 4 * c4);
+    }
+  const T* w = reinterpret_cast<const T*>(a.q_norm_weight);
+  u32x4 wl_raw[H2], wh_raw[H2];
+  if (w) {
+#pragma unroll
+    for (int s = 0; s < H2; ++s) {
+      wl_raw[s] = load_chunk(w + 16 * s + 8 * hf).raw;
+      wh_raw[s] = load_chunk(w + D / 2 + 16 * s + 8 * hf).raw;
+    }
+  }
   float lo[H2][8], hi[H2][8], cs[2 * H2];
   float own[H2];
 #pragma unroll
@@ -256,15 +279,13 @@ __device__ __forceinline__ void fuse_q_producer(const FwdArgs& a, u32x4 (&qf)[(D
     cs[2 * s + hf] = own[s];
     cs[2 * s + (hf ^ 1)] = other;
   }
-  if (!live) return;  // rows past the end stay zero
-  if (a.q_norm_weight) {
+  if (w) {
     const float inv = qk_rms_inv(qk_butterfly_sum(cs), D, a.eps);
-    const T* w = reinterpret_cast<const T*>(a.q_norm_weight);
 #pragma unroll
     for (int s = 0; s < H2; ++s) {
       float wl[8], wh[8];
-      chunk_unpack(load_chunk(w + 16 * s + 8 * hf), wl);
-      chunk_unpack(load_chunk(w + D / 2 + 16 * s + 8 * hf), wh);
+      chunk_unpack(Chunk<T>{wl_raw[s]}, wl);
+      chunk_unpack(Chunk<T>{wh_raw[s]}, wh);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         lo[s][i] = lo[s][i] * inv * wl[i];
@@ -272,26 +293,21 @@ __device__ __forceinline__ void fuse_q_producer(const FwdArgs& a, u32x4 (&qf)[(D
       }
     }
   }
-  // table entries [pos][2j], j = 16s + 8hf + i
-  const float* sn = a.rope_sin + (long)pos * D;
-  const float* cn = a.rope_cos + (long)pos * D;
+  if (!live) return;  // rows past the end stay zero
   typedef T T8 __attribute__((ext_vector_type(8)));
 #pragma unroll
   for (int s = 0; s < H2; ++s) {
     T8 rl, rh;
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-      const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + 32 * s + 16 * hf + 4 * c4);
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(cn + 32 * s + 16 * hf + 4 * c4);
+    for (int c4 = 0; c4 < 4; ++c4)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int i = 2 * c4 + e;
         float ro, rv;
-        qk_rope(lo[s][i], hi[s][i], k4[2 * e], s4[2 * e], ro, rv);
+        qk_rope(lo[s][i], hi[s][i], k4[s][c4][2 * e], s4[s][c4][2 * e], ro, rv);
         rl[i] = from_f32<T>(ro);
         rh[i] = from_f32<T>(rv);
       }
-    }
     qf[s] = __builtin_bit_cast(u32x4, rl);
     qf[s + H2] = __builtin_bit_cast(u32x4, rh);
   }
@@ -456,15 +472,16 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       if (qi < q_n && 16 * s + 8 * hf < D) val = *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * hf);
       qf[s] = val;
     }
-    if constexpr (CAUSAL && (D == 64 || D == 128)) {
-      if (a.rope_sin) fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, hf);
-    }
   }
 
   // Stages 0..2 up front; wait for stage 0 (younger stages may stay in flight).
   issue_stage(0);
   if (n_tiles >= 1) issue_stage(1);
   if (n_tiles >= 2) issue_stage(2);
+  // The fused Q producer works while the first stages are in flight.
+  if constexpr (CAUSAL && (D == 64 || D == 128)) {
+    if (a.rope_sin) fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
+  }
   if (n_tiles >= 2) wait_vmcnt<8>();
   else wait_vmcnt<4>();
   step_barrier();

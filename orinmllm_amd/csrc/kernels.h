@@ -105,4 +105,9 @@ hipError_t launch_rope_cache(float* sin_cache, float* cos_cache, int head_size, 
 hipError_t launch_vision_qkv(const void* qkv, const void* cos_t, const void* sin_t, void* q,
                              void* k, void* v, int N, int H, int d, int dtype, hipStream_t stream);
 
+// Attention output projection (outproj.hip): out[b, k] = scale * sum_m in[b, m] * w[k, m].
+// Returns 0, -1 (library error) or -2 (dtype).
+int output_projection(const void* input, const void* weight, void* output, int batch, int in_dim,
+                      int out_dim, float scale, int dtype, hipStream_t stream);
+
 }  // namespace orin

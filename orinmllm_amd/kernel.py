@@ -338,6 +338,18 @@ KV_TO_PAGED = 0
 KV_TO_CONTIGUOUS = 1
 
 
+def batched_matmul_kernel_cu(input, weight, output, batch_size, scale=1.0, config=None):
+    """kernel::batched_matmul_kernel_cu (matmul_kernel.cuh:15-41): output [batch, out_dim] =
+    scale * input [batch, in_dim] @ weight[out_dim, in_dim]^T (the wo projection)."""
+    out_dim, in_dim = weight.shape
+    if input.numel() != batch_size * in_dim or output.numel() != batch_size * out_dim:
+        raise ValueError("input / output sizes do not match the weight")
+    dt = _dtype(input, weight, output)
+    _lib.check("orin_batched_matmul", _lib.load().orin_batched_matmul(
+        _ptr(input, "input"), _ptr(weight, "weight"), _ptr(output, "output"), batch_size, in_dim,
+        out_dim, float(scale), dt, _stream(config)))
+
+
 def copy_to_kv_cache_kernel(kv_cache, src, pos, kv_dim, layer_idx, seq_len, config=None):
     """kernel::copy_to_kv_cache_kernel / copy_to_kv_cache_kernel_fp16
     (kuiper/source/op/kernels/cuda/kv_cache_kernel.cuh:24-33): src [kv_dim] goes to row

@@ -90,11 +90,11 @@ def test_producer_arguments_are_rejected():
                                      None) == INV
     assert lib.orin_rope_sin_cos_cache(FAKE, FAKE, 128, 0, 1e6, None) == INV
     assert lib.orin_rope_sin_cos_cache(FAKE, FAKE, 128, 64, -1.0, None) == INV
-    # producer: the tokens must fit the cache; head sizes 128 / 256 only
+    # producer: the tokens must fit the cache; head sizes 64 / 128 / 256 only
     assert lib.orin_qk_norm_rope(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0, 64, 60,
                                  None, 8, 32, 8, 128, 1e-6, F16, None) == INV
     assert lib.orin_qk_norm_rope(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0, 64, 0,
-                                 None, 8, 32, 8, 64, 1e-6, F16, None) == UNS
+                                 None, 8, 32, 8, 96, 1e-6, F16, None) == UNS
     assert lib.orin_vision_split_rope_transpose(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1024, 16, 71,
                                                 _lib.DTYPE_BF16, None) == INV
 
