@@ -55,6 +55,9 @@ def parse():
                     help="skip the decode with every KV length 4096")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the C1 / C2 / C3-bf16 / C5 timings")
+    ap.add_argument("--only-other-configs", action="store_true",
+                    help="time only the C1 / C2 / C3-bf16 / C5 configs and print them as one "
+                         "JSON object (for profiling those kernels; not the bench line)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 512 MiB device copy (the reference traffic for the "
                          "FETCH_SIZE / WRITE_SIZE counters)")
@@ -425,6 +428,9 @@ def main():
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xC3)
+    if args.only_other_configs:
+        print(json.dumps({"other_configs": time_other_configs(K, gen, reps=args.reps)}))
+        return 0
     pf = make_prefill(dtype, gen)
     dc = make_decode(dtype, gen, args.pools)
     ws_bytes = K.decode_workspace_size(dc["B"], dc["Hq"], dc["Hkv"], dc["d"], dc["maxlen"])
