@@ -6,7 +6,8 @@ import torch
 
 from oracle import oracle
 from orinmllm_amd import kernel as K
-from tests.util import assert_fp32_close, assert_lowp_close, normal, quantize, rel_error
+from tests.util import (assert_fp32_close, assert_fp32_elementwise, assert_lowp_close,
+                        fp64_decode, normal, quantize, rel_error)
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +46,11 @@ def test_c1_fp32_mha_kernel(gpu_pos):
                         dev(kc), dev(vc))
     torch.cuda.synchronize()
     assert_fp32_close(host(out), ref, head_size, what="C1")
+    # Element by element against float64: 1e-4 relative (floor 1e-6 of the head max).
+    truth = fp64_decode(q, kc[layer, : pos + 1].reshape(pos + 1, head_num, head_size),
+                        vc[layer, : pos + 1].reshape(pos + 1, head_num, head_size), head_num, 1,
+                        head_size)
+    assert_fp32_elementwise(host(out), truth, head_size, what="C1 vs fp64")
     # The reference's own element-wise metric (bench_mha_kernels.cu:467-477), reported:
     # it is dominated by near-zero outputs, see assert_fp32_close.
     print(f"C1 element-wise rel error (reference metric): {rel_error(host(out), ref):.3g}")
@@ -78,6 +84,7 @@ def test_fp32_mha_qwen3_shape(pos):
         truth[h] = (p / p.sum()) @ V[:, h // kv_mul]
     truth = truth.ravel()
     assert np.abs(host(out) - truth).max() <= 2 * np.abs(ref - truth).max() + 1e-7
+    assert_fp32_elementwise(host(out), truth, d, what=f"pos {pos} vs fp64")
 
 
 # ---------------------------------------------------------------- flash decode

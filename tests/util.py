@@ -37,6 +37,32 @@ def assert_fp32_close(got, ref, head_size, tol=1e-4, what=""):
     assert nw <= tol and ew <= tol, f"{what}: norm-wise {nw:.3g}, element-wise {ew:.3g} > {tol}"
 
 
+def assert_fp32_elementwise(got, truth, head_size, rtol=1e-4, floor=1e-6, what=""):
+    """fp32 bar element by element against an fp64 evaluation of the same inputs:
+    |got - truth| <= rtol * |truth| + floor * max|truth of the head| for every output.
+    The floor (1e-6 of the head's largest output, ~8 fp32 ulps of it) only matters for
+    outputs that cancel to near zero."""
+    g = np.asarray(got, np.float64).reshape(-1, head_size)
+    t = np.asarray(truth, np.float64).reshape(-1, head_size)
+    bound = rtol * np.abs(t) + floor * np.abs(t).max(axis=1, keepdims=True)
+    bad = np.abs(g - t) > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outputs outside "
+                           f"{rtol} relative + {floor} of the head max")
+
+
+def fp64_decode(q, k_rows, v_rows, head_num, kv_mul, d):
+    """Softmax(q k^T / sqrt(d)) v per head in float64; k_rows / v_rows [n, kv_heads, d]."""
+    Q = np.asarray(q, np.float64).reshape(head_num, d)
+    Kd = np.asarray(k_rows, np.float64)
+    V = np.asarray(v_rows, np.float64)
+    out = np.zeros((head_num, d))
+    for h in range(head_num):
+        s = Kd[:, h // kv_mul] @ Q[h] / np.sqrt(d)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ V[:, h // kv_mul]
+    return out.ravel()
+
+
 def assert_lowp_close(got, ref, atol=2e-3, rtol=1e-2, what=""):
     """fp16/bf16 bar: |got - ref| <= atol + rtol*|ref| against the fp32-accumulated
     oracle on the same (16-bit) inputs."""
