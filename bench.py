@@ -55,6 +55,8 @@ def parse():
                     help="skip the decode with every KV length 4096")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the C1 / C2 / C3-bf16 / C5 timings")
+    ap.add_argument("--no-pipeline", action="store_true",
+                    help="skip the C3 producer + prefill + wo pipeline timings")
     ap.add_argument("--only-other-configs", action="store_true",
                     help="time only the C1 / C2 / C3-bf16 / C5 configs and print them as one "
                          "JSON object (for profiling those kernels; not the bench line)")
@@ -521,8 +523,9 @@ def main():
         out["decode_kv4096"] = time_decode_uniform(K, dtype, gen, args.pools)
     if not args.no_other_configs:
         out["other_configs"] = time_other_configs(K, gen)
-    if not args.no_producers:
+    if not args.no_producers and not args.no_pipeline:
         out["c3_pipeline"] = time_fused_pipeline(K, dtype, gen)
+    if not args.no_producers:
         out["producers"] = time_producers(K, make_producers(dtype, gen))
         for name, rec in out["producers"].items():
             rec["traffic"] = _bytes(traffic.get(name))

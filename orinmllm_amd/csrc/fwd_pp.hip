@@ -313,7 +313,9 @@ __device__ __forceinline__ void fuse_q_producer(const FwdArgs& a, u32x4 (&qf)[(D
   }
 }
 
-template <typename T, bool CAUSAL, int D>
+// FQ: the fused Q producer variant (a.rope_sin set), a separate instance so that its
+// registers do not weigh on the plain kernel.
+template <typename T, bool CAUSAL, int D, bool FQ>
 __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   static_assert(D % 8 == 0 && D <= PD, "head size: a multiple of 8 up to 128");
   constexpr int QS = (D + 15) / 16;  // 16-wide slices of the QK contraction (zero-padded)
@@ -479,9 +481,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   if (n_tiles >= 1) issue_stage(1);
   if (n_tiles >= 2) issue_stage(2);
   // The fused Q producer works while the first stages are in flight.
-  if constexpr (CAUSAL && (D == 64 || D == 128)) {
-    if (a.rope_sin) fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
-  }
+  if constexpr (FQ && CAUSAL && (D == 64 || D == 128))
+    fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
   if (n_tiles >= 2) wait_vmcnt<8>();
   else wait_vmcnt<4>();
   step_barrier();
@@ -797,18 +798,25 @@ hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
   else if (CAUSAL) blocks = (long)((a.n_q + PBM - 1) / PBM) * a.Hq;
   else blocks = (long)a.n_seg * ((a.max_seqlen + PBM - 1) / PBM) * a.Hq;
   if (blocks <= 0) return hipSuccess;
-  static unsigned long long configured = 0;
+  constexpr bool kFusable = CAUSAL && (D == 64 || D == 128);
+  const bool fq = kFusable && a.rope_sin != nullptr;
+  const void* fn = fq ? (const void*)fwd_pp_kernel<T, CAUSAL, D, kFusable>
+                      : (const void*)fwd_pp_kernel<T, CAUSAL, D, false>;
+  static unsigned long long configured[2] = {0, 0};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  if (dev >= 64 || !(__atomic_load_n(&configured, __ATOMIC_ACQUIRE) & (1ull << dev))) {
-    e = hipFuncSetAttribute((const void*)fwd_pp_kernel<T, CAUSAL, D>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, PLDS_BYTES);
+  if (dev >= 64 || !(__atomic_load_n(&configured[fq], __ATOMIC_ACQUIRE) & (1ull << dev))) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, PLDS_BYTES);
     if (e != hipSuccess) return e;
-    if (dev < 64) __atomic_fetch_or(&configured, 1ull << dev, __ATOMIC_RELEASE);
+    if (dev < 64) __atomic_fetch_or(&configured[fq], 1ull << dev, __ATOMIC_RELEASE);
   }
-  hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D>), dim3((unsigned)blocks), dim3(PTHREADS),
-                     PLDS_BYTES, stream, a);
+  if (fq)
+    hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D, kFusable>), dim3((unsigned)blocks),
+                       dim3(PTHREADS), PLDS_BYTES, stream, a);
+  else
+    hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D, false>), dim3((unsigned)blocks),
+                       dim3(PTHREADS), PLDS_BYTES, stream, a);
   if (CAUSAL && a.key_chunk_tiles > 0) {
     const int nqb = (a.n_q + PBM - 1) / PBM;
     hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * (PBM / kMergeRows))),
