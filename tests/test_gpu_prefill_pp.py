@@ -94,3 +94,27 @@ def test_pp_key_split_aliased_output():
     rows = sample_rows(S, 60, rng)
     ref = oracle.prefill_causal(0, q, kc, vc, Hq, Hkv, d, rows=rows, nthreads=8)
     assert_lowp_close(out[rows], ref, what="key split aliased")
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+def test_pp_launches_are_bit_reproducible(kind):
+    """The same launch on the same inputs gives the same bits, causal (with and without the
+    key split) and varlen: the kernels hold no atomics or order-dependent reductions."""
+    rng = np.random.default_rng(23)
+    H, d = 16, 128
+    cu = np.array([0, 1024, 2048, 2900, 3924], np.int32)
+    q, k, v = vision_inputs(rng, cu, H, d, kind)
+    N = int(cu[-1])
+    args = [dev(q, kind), dev(k, kind), dev(v, kind)]
+    dcu = torch.from_numpy(cu).cuda()
+    outs = []
+    for _ in range(3):
+        out = torch.zeros(N, H * d, device="cuda", dtype=TORCH[kind])
+        K.vision_attention_varlen_cu(*args, out, dcu, 1024, H, d)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    for S, Hq, Hkv in [(4096, 32, 8), (2048, 12, 2)]:  # one plain launch, one key split
+        res = [run_prefill(kind, 0, S, Hq, Hkv, d, S, 1, 0, np.random.default_rng(5))[3]
+               for _ in range(2)]
+        assert np.array_equal(res[0], res[1]), f"causal S {S}"
