@@ -33,7 +33,8 @@
 // Key split.  A causal launch with fewer 256-query blocks than CUs is bounded by its
 // longest block; the host then cuts each block's keys before its diagonal into chunks
 // (key_chunk_tiles), each run by its own workgroup, and fwd_pp_merge combines the
-// chunks' fp32 partials (unnormalised O, m and l) in a second launch.
+// chunks' partials (O / l in fp16 for fp16 inputs, fp32 otherwise; fp32 m and l) in a
+// second launch.
 #include "common.h"
 #include "kernels.h"
 
@@ -187,10 +188,15 @@ __host__ __device__ inline int pp_items(const FwdArgs& a, int C) {
   for (int b = 0; b < nqb; ++b) n += pp_block_chunks(a, b, C);
   return n;
 }
-// Workspace of a key split: unnormalised O rows [items * Hq * PBM][head_size] fp32, then
-// (m, l) [items * Hq * PBM][2] fp32.  Offsets in floats.
-__host__ __device__ inline long pp_ml_offset(const FwdArgs& a, int D) {
-  return (long)pp_items(a, a.key_chunk_tiles) * a.Hq * PBM * D;
+// Workspace of a key split: normalised O rows (O / l) [items * Hq * PBM][head_size] in the
+// partial type, then (m, l) [items * Hq * PBM][2] fp32.  The partial type is fp16 for fp16
+// inputs (|O / l| <= max |V|, and fp16 keeps 11 bits: one more rounding of 2^-12 relative)
+// and fp32 for bf16 inputs (a bf16 partial would add a rounding as large as the output's).
+// Offsets in floats.
+template <typename T>
+using PartT = typename std::conditional<std::is_same<T, f16>::value, f16, float>::type;
+__host__ __device__ inline long pp_ml_offset(const FwdArgs& a, int D, int part_bytes) {
+  return (long)pp_items(a, a.key_chunk_tiles) * a.Hq * PBM * D * part_bytes / 4;
 }
 
 // Order of the MFMAs of one phase: QK steps (2 per 16-wide slice of the head) and PV steps
@@ -695,29 +701,34 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 
   // ------------------------------------------------------------ normalise and store
   const float l_tot = l_run + partner32(l_run);
+  const float inv = 1.f / l_tot;
   if (partial) {
-    // Partial of this key chunk per query row: unnormalised O and (m, l), fp32.
+    // Partial of this key chunk per query row: O / l in the partial type, and (m, l) fp32.
+    using PT = PartT<T>;
     const long row = (long)blockIdx.x * PBM + (qi - q_lo);
     if (qi < q_n) {
-      float* pr = a.ws + row * D;
+      PT* pr = reinterpret_cast<PT*>(a.ws) + row * D;
 #pragma unroll
       for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
           const int d0 = t * 32 + 8 * rg + 4 * hf;
           if (d0 >= D) continue;
-          *reinterpret_cast<f32x4*>(pr + d0) =
-              f32x4{oacc[t][4 * rg], oacc[t][4 * rg + 1], oacc[t][4 * rg + 2], oacc[t][4 * rg + 3]};
+          const float o0 = oacc[t][4 * rg] * inv, o1 = oacc[t][4 * rg + 1] * inv;
+          const float o2 = oacc[t][4 * rg + 2] * inv, o3 = oacc[t][4 * rg + 3] * inv;
+          if constexpr (sizeof(PT) == 2)
+            *reinterpret_cast<u32x2*>(pr + d0) = u32x2{pack2<T>(o0, o1), pack2<T>(o2, o3)};
+          else
+            *reinterpret_cast<f32x4*>(pr + d0) = f32x4{o0, o1, o2, o3};
         }
       if (hf == 0) {
-        float* ml = a.ws + pp_ml_offset(a, D) + row * 2;
+        float* ml = a.ws + pp_ml_offset(a, D, sizeof(PT)) + row * 2;
         ml[0] = m_use;
         ml[1] = l_tot;
       }
     }
     return;
   }
-  const float inv = 1.f / l_tot;
   if (qi < q_n) {
     T* op = reinterpret_cast<T*>(a.o) + (long)(seg_start + qi) * a.o_tok_stride +
             (long)head * a.o_head_stride;
@@ -735,7 +746,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 }
 
 // Merge the key-chunk partials of the split query blocks:
-// O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  A thread owns 8 dimensions of one row
+// O = sum_c w_c (O_c / l_c) / sum_c w_c with w_c = 2^(m_c - M) l_c.  A thread owns 8 dimensions of one row
 // (16 rows per workgroup, a row's threads neighbours so a wave reads whole rows); every
 // load it needs is issued before any is used.
 constexpr int kMergeMaxChunks = 8;
@@ -756,19 +767,22 @@ __global__ void __launch_bounds__(kMergeRows * ((D + 7) / 8)) fwd_pp_merge(FwdAr
   const int nqb = (a.n_q + PBM - 1) / PBM;
   int item0 = 0;  // the items of blocks qb+1 .. nqb-1 come first
   for (int b = nqb - 1; b > qb; --b) item0 += pp_block_chunks(a, b, C);
-  const float* ml = a.ws + pp_ml_offset(a, D);
+  using PT = PartT<T>;
+  const float* ml = a.ws + pp_ml_offset(a, D, sizeof(PT));
+  const PT* po = reinterpret_cast<const PT*>(a.ws);
   const int d0 = 8 * part;
   float m[kMergeMaxChunks], l[kMergeMaxChunks];
-  f32x4 x[kMergeMaxChunks][2];
+  u32x4 x[kMergeMaxChunks][sizeof(PT) / 2];  // the 8 partial values of each chunk
 #pragma unroll
   for (int c = 0; c < kMergeMaxChunks; ++c) {
     const long row = ((long)(item0 + min(c, n_ch - 1)) * a.Hq + head) * PBM + r;
     m[c] = c < n_ch ? ml[row * 2] : -INFINITY;
     l[c] = c < n_ch ? ml[row * 2 + 1] : 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      x[c][j] = (c < n_ch && d0 + 4 * j < D) ? *reinterpret_cast<const f32x4*>(a.ws + row * D + d0 + 4 * j)
-                                             : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < (int)sizeof(PT) / 2; ++j)
+      x[c][j] = (c < n_ch && d0 < D)
+                    ? *reinterpret_cast<const u32x4*>(po + row * D + d0 + j * (16 / sizeof(PT)))
+                    : u32x4{0u, 0u, 0u, 0u};
   }
   float M = m[0];
 #pragma unroll
@@ -778,10 +792,21 @@ __global__ void __launch_bounds__(kMergeRows * ((D + 7) / 8)) fwd_pp_merge(FwdAr
   for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
   for (int c = 0; c < kMergeMaxChunks; ++c) {
-    const float w = c < n_ch ? fast_exp2(m[c] - M) : 0.f;
-    W = __builtin_fmaf(w, l[c], W);
+    const float w = c < n_ch ? fast_exp2(m[c] - M) * l[c] : 0.f;
+    W += w;
+    float xv[8];
+    if constexpr (sizeof(PT) == 2) {
+      chunk_unpack(Chunk<f16>{x[c][0]}, xv);
+    } else {
+      const f32x4 lo = __builtin_bit_cast(f32x4, x[c][0]), hi = __builtin_bit_cast(f32x4, x[c][1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(w, x[c][e >> 2][e & 3], o[e]);
+      for (int e = 0; e < 4; ++e) {
+        xv[e] = lo[e];
+        xv[e + 4] = hi[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(w, xv[e], o[e]);
   }
   const float inv = 1.f / W;
   if (d0 >= D) return;
@@ -863,7 +888,8 @@ int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
     const int diag_extra = longest - pp_block_diag(a, nqb - 1);
     if (3 * (C + diag_extra) > 2 * longest) return 0;
     const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
-    *ws_bytes = rows * a.head_size * sizeof(float) + rows * 2 * sizeof(float);
+    const size_t part_bytes = dtype == kF16 ? 2 : 4;  // PartT
+    *ws_bytes = rows * a.head_size * part_bytes + rows * 2 * sizeof(float);
     return C;
   }
   return 0;

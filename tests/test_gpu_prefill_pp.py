@@ -9,7 +9,7 @@ from oracle import oracle
 from orinmllm_amd import kernel as K
 from tests.test_gpu_prefill import run_prefill, sample_rows
 from tests.test_gpu_vision import TORCH, dev, vision_inputs
-from tests.util import assert_lowp_close
+from tests.util import assert_lowp_close, quantize
 
 pytestmark = pytest.mark.gpu
 
@@ -118,3 +118,35 @@ def test_pp_launches_are_bit_reproducible(kind):
         res = [run_prefill(kind, 0, S, Hq, Hkv, d, S, 1, 0, np.random.default_rng(5))[3]
                for _ in range(2)]
         assert np.array_equal(res[0], res[1]), f"causal S {S}"
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+def test_key_split_close_to_unsplit(kind):
+    """The key split's partials (O / l in fp16 for fp16 inputs, fp32 for bf16) add at most
+    about one rounding of the output type: C2 (12 heads, split) against the same heads
+    launched three times over (36 heads, 288 blocks: no split)."""
+    rng = np.random.default_rng(31)
+    S, Hq, Hkv, d = 2048, 12, 2, 128
+    q = quantize(rng.standard_normal((S, Hq * d)).astype(np.float32), kind)
+    k = quantize(rng.standard_normal((S, Hkv * d)).astype(np.float32), kind)
+    v = quantize(rng.standard_normal((S, Hkv * d)).astype(np.float32), kind)
+    dt = TORCH[kind]
+
+    def run(qh, kh, vh, hq, hkv):
+        qd = torch.from_numpy(qh).to(dt).cuda()
+        out = torch.zeros_like(qd)
+        K.flash_attention_prefill_cu(0, S, hq, hkv, d, hq // hkv, 0, S, hkv * d, qd, out,
+                                     torch.from_numpy(kh).to(dt).cuda(),
+                                     torch.from_numpy(vh).to(dt).cuda())
+        torch.cuda.synchronize()
+        return out.float().cpu().numpy()
+
+    split = run(q, k, v, Hq, Hkv)
+    whole = run(np.tile(q, (1, 3)), np.tile(k, (1, 3)), np.tile(v, (1, 3)), 3 * Hq, 3 * Hkv)
+    ulp = 2.0 ** -10 if kind == "fp16" else 2.0 ** -7  # one unit in the last place, relative
+    for c in range(3):
+        part = whole[:, c * Hq * d:(c + 1) * Hq * d]
+        err = np.abs(split - part)
+        # Chunks sum their keys in another order than the whole row: the difference is a
+        # few roundings of the output type, relative to outputs of order one.
+        assert (err <= 2 * ulp * np.abs(part) + 0.5 * ulp).all(), f"{kind} copy {c}: {err.max():.3g}"
