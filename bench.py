@@ -124,14 +124,16 @@ def make_decode(dtype, gen, pools, layout=1, uniform_len=None):
 
 def time_decode_uniform(K, dtype, gen, pools, reps=50):
     """The batch-32 paged decode with every KV length 4096 (the length the decode target
-    is stated at), timed like the C4 decode: automatic split size, and 1024-token splits
-    passed explicitly (split_tokens is part of the API for callers that know their
-    lengths)."""
+    is stated at), timed like the C4 decode: automatic split size (from max_context_len
+    alone), the split orin_attn_decode_split_tokens_for_total picks from the batch's total
+    length (a serving loop knows it on the host), and 1024-token splits passed explicitly."""
     import torch
     dc = make_decode(dtype, gen, pools, uniform_len=4096)
     stream = torch.cuda.current_stream()
     out = {"kv_bytes_per_call": dc["kv_bytes"]}
-    for name, st in [("auto_split", 0), ("split_1024", 1024)]:
+    hint = K.decode_split_tokens_for_total(dc["B"], dc["Hq"], dc["Hkv"], dc["maxlen"],
+                                           int(dc["lens"].sum()))
+    for name, st in [("auto_split", 0), ("split_for_total", hint), ("split_1024", 1024)]:
         nb = K.decode_workspace_size(dc["B"], dc["Hq"], dc["Hkv"], dc["d"], dc["maxlen"], st)
         ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
 
@@ -144,7 +146,7 @@ def time_decode_uniform(K, dtype, gen, pools, reps=50):
         ms = per_launch(run, reps, 10, stream, indexed=True)["median_ms"]
         gbs = dc["kv_bytes"] / (ms * 1e-3) / 1e9
         out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "split_tokens": st}
     del dc
     torch.cuda.empty_cache()
     return out

@@ -219,15 +219,29 @@ int orin_attn_workspace_release(void);
  * context_lens (device, [batch]) gives each row's KV length; max_context_len bounds
  * them (it sets the launch shape).  A row whose length exceeds max_context_len (the host
  * cannot see device lengths) gets NaN outputs instead of attention over a truncated
- * prefix; the same holds for *pos_ptr >= max_seq_len in the gpu-pos entry points.  split_tokens: tokens per split (multiple of 64,
- * else ORIN_ERR_INVALID_ARG), 0 = automatic.  Workspace: orin_attn_decode_workspace_size bytes (may be NULL when
- * that is 0).
+ * prefix; the same holds for *pos_ptr >= max_seq_len in the gpu-pos entry points.
+ * split_tokens: tokens per split (multiple of 64, else ORIN_ERR_INVALID_ARG), 0 =
+ * automatic (from max_context_len alone; orin_attn_decode_split_tokens_for_total uses the
+ * batch's total length too).  Workspace: orin_attn_decode_workspace_size bytes (may be NULL
+ * when that is 0).
  */
 size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t kv_head_num,
                                        int32_t head_size, int32_t max_context_len,
                                        int32_t split_tokens);
 int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t kv_head_num,
                                       int32_t max_context_len, int32_t split_tokens);
+/*
+ * Split size for a batched decode whose total KV length sum_context_len (the sum of the
+ * rows' context lengths) the caller knows on the host -- a serving loop keeps it; no
+ * reference counterpart.  When every row is close to max_context_len (sum >= 0.9 * batch *
+ * max_context_len) the launch gets a few long splits per row (one round of the
+ * workgroups the device holds at once), which streams faster than the automatic choice;
+ * otherwise it returns the automatic choice.  Pass the result as split_tokens (and to
+ * orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid arguments.
+ */
+int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,
+                                                int32_t kv_head_num, int32_t max_context_len,
+                                                int64_t sum_context_len);
 int orin_attn_decode(const void* query, const void* key_cache, const void* value_cache,
                      void* out, int32_t batch, int32_t head_num, int32_t kv_head_num,
                      int32_t head_size, int64_t cache_batch_stride, int64_t cache_tok_stride,

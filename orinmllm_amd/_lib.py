@@ -45,6 +45,7 @@ SIGNATURES = {
     "orin_attn_workspace_release": (C.c_int, []),
     "orin_attn_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "orin_attn_decode_split_tokens": (i32, [i32, i32, i32, i32, i32]),
+    "orin_attn_decode_split_tokens_for_total": (i32, [i32, i32, i32, i32, i64]),
     "orin_attn_decode": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, i64, i64, vp, i32, i32, f32, i32, vp, sz, vp]),
     "orin_attn_decode_paged": (C.c_int, [vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, i32, i32, vp, i32, i32, f32, i32, vp, sz, vp]),
     "orin_vision_attention_pretransposed": (C.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, f32, i32, vp]),

@@ -240,6 +240,17 @@ def decode_workspace_size(batch, head_num, kv_head_num, head_size, max_context_l
         batch, head_num, kv_head_num, head_size, max_context_len, split_tokens))
 
 
+def decode_split_tokens_for_total(batch, head_num, kv_head_num, max_context_len,
+                                  sum_context_len):
+    """Split size (pass it as split_tokens) for a batched decode whose total KV length the
+    caller knows on the host; the automatic choice unless the rows are near-uniform."""
+    st = int(_lib.load().orin_attn_decode_split_tokens_for_total(
+        batch, head_num, kv_head_num, max_context_len, int(sum_context_len)))
+    if st <= 0:
+        raise _lib.OrinAttnError("orin_attn_decode_split_tokens_for_total", _lib.ERR_INVALID_ARG)
+    return st
+
+
 def _workspace(nbytes, workspace, device):
     if nbytes == 0:
         return None, 0

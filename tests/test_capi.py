@@ -131,3 +131,16 @@ def test_missing_library_fails_loudly(tmp_path):
             _lib.load(str(tmp_path / "missing.so"))
     finally:
         _lib._lib = saved
+
+
+def test_split_tokens_for_total():
+    """Near-uniform batches get one round of long splits; ragged ones the automatic size;
+    bad arguments 0.  Host-only (the CU count query falls back to 256 without a GPU)."""
+    lib = _lib.load()
+    f = lib.orin_attn_decode_split_tokens_for_total
+    auto = lib.orin_attn_decode_split_tokens(32, 32, 8, 4096, 0)
+    ragged = f(32, 32, 8, 4096, 74949)
+    uniform = f(32, 32, 8, 4096, 32 * 4096)
+    assert ragged == auto
+    assert uniform % 64 == 0 and uniform > auto
+    assert f(0, 32, 8, 4096, 1) == 0 and f(32, 32, 7, 4096, 1) == 0 and f(32, 32, 8, 4096, -1) == 0
