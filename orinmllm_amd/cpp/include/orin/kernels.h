@@ -98,6 +98,12 @@ void vision_attention_pretransposed_cu(const tensor::Tensor& q_trans,
                                        tensor::Tensor& out_transposed, tensor::Tensor& scores,
                                        int num_tokens, int num_heads, int head_dim,
                                        float softmax_scale, const CudaConfig* config);
+// matmul_kernel.cuh:37-41: output [batch, out] = scale * input [batch, in] . weight^T,
+// weight [out, in] -- the wo projection after the batched attention (qwen_base.cpp:464-474).
+void batched_matmul_kernel_cu_pure_fp16(const tensor::Tensor& input,
+                                         const tensor::Tensor& weight,
+                                         const tensor::Tensor& output, int32_t batch_size,
+                                         float scale = 1.f, const CudaConfig* config = nullptr);
 void fused_split_rope_transpose_cu(const tensor::Tensor& qkv, const tensor::Tensor& cos_cache,
                                    const tensor::Tensor& sin_cache, tensor::Tensor& q_trans,
                                    tensor::Tensor& k_trans, tensor::Tensor& v_trans,

@@ -180,6 +180,20 @@ void vision_attention_pretransposed_cu(const tensor::Tensor& q_trans,
              stream_of(config)));
 }
 
+void batched_matmul_kernel_cu_pure_fp16(const tensor::Tensor& input,
+                                         const tensor::Tensor& weight,
+                                         const tensor::Tensor& output, int32_t batch_size,
+                                         float scale, const CudaConfig* config) {
+  if (weight.dims_size() != 2) {
+    record("batched_matmul_kernel_cu_pure_fp16", ORIN_ERR_INVALID_ARG);
+    return;
+  }
+  record("batched_matmul_kernel_cu_pure_fp16",
+         orin_batched_matmul(input.raw_ptr(), weight.raw_ptr(), output.raw_ptr(), batch_size,
+                             weight.get_dim(1), weight.get_dim(0), scale,
+                             common_dtype({&input, &weight, &output}), stream_of(config)));
+}
+
 void fused_split_rope_transpose_cu(const tensor::Tensor& qkv, const tensor::Tensor& cos_cache,
                                    const tensor::Tensor& sin_cache, tensor::Tensor& q_trans,
                                    tensor::Tensor& k_trans, tensor::Tensor& v_trans,

@@ -374,4 +374,28 @@ TEST(GpuCopyToKVCacheLayer, Fp16RowLandsAtDevicePosition) {
   EXPECT_TRUE(close(all, want, 0.f, 0.f, "kv cache row"));
 }
 
+TEST(GpuKernels, Fp16WoProjectionMatchesFp32Reference) {
+  // batched_matmul_kernel_cu_pure_fp16 (the wo projection): out = 0.5 * in . w^T.
+  ASSERT_TRUE(gpu_ok());
+  const DataType dt = DataType::kDataTypeFp16;
+  const int B = 64, in_dim = 256, out_dim = 128;
+  std::vector<float> xh = normal((size_t)B * in_dim, 51), wh = normal((size_t)out_dim * in_dim, 52);
+  DevTensor x(xh, {B, in_dim}, dt), w(wh, {out_dim, in_dim}, dt);
+  DevTensor o((size_t)B * out_dim, {B, out_dim}, dt);
+  kernel::CudaConfig cfg;
+  kernel::batched_matmul_kernel_cu_pure_fp16(x.t, w.t, o.t, B, 0.5f, &cfg);
+  ASSERT_TRUE(static_cast<bool>(kernel::last_status()));
+  ASSERT_TRUE(hipDeviceSynchronize() == hipSuccess);
+  const std::vector<float>& xs = xh;  // rounded to fp16 by DevTensor
+  const std::vector<float>& ws = wh;
+  std::vector<float> ref((size_t)B * out_dim);
+  for (int b = 0; b < B; ++b)
+    for (int k = 0; k < out_dim; ++k) {
+      double acc = 0;
+      for (int m = 0; m < in_dim; ++m) acc += (double)xs[(size_t)b * in_dim + m] * ws[(size_t)k * in_dim + m];
+      ref[(size_t)b * out_dim + k] = (float)(0.5 * acc);
+    }
+  EXPECT_TRUE(close(download(o.buf, (size_t)B * out_dim, dt), ref, 2e-2f, 1e-2f, "wo"));
+}
+
 int main(int argc, char** argv) { return mini_test::run_all(argc, argv); }
