@@ -234,9 +234,11 @@ int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t k
  * Split size for a batched decode whose total KV length sum_context_len (the sum of the
  * rows' context lengths) the caller knows on the host -- a serving loop keeps it; no
  * reference counterpart.  When every row is close to max_context_len (sum >= 0.9 * batch *
- * max_context_len) the launch gets a few long splits per row (one round of the
- * workgroups the device holds at once), which streams faster than the automatic choice;
- * otherwise it returns the automatic choice.  Pass the result as split_tokens (and to
+ * max_context_len) the launch gets one split per row when the (row, kv head) units fill
+ * the CUs in rounds at least 90% full (16-bit K/V then run one whole-CU workgroup per unit
+ * and no merge), else a few long splits per row (one round of the workgroups the device
+ * holds at once); both stream faster than the automatic choice.  Otherwise it returns
+ * the automatic choice.  Pass the result as split_tokens (and to
  * orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid arguments.
  */
 int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,

@@ -170,6 +170,7 @@ int kuiper_decode_split(int head_num, int kv_head_num, int head_size, int max_le
 int run_decode(DecodeArgs& a, int dtype, int max_len, hipStream_t stream) {
   a.max_splits = n_splits(max_len, a.split_tokens);
   if (a.max_splits <= 1) a.max_splits = 1;
+  a.wide = a.max_splits == 1;
   a.len_cap = max_len > 0 ? max_len : (1 << 30);
   return hip_status(launch_decode(a, dtype, stream));
 }
@@ -607,11 +608,18 @@ int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,
                                                       max_context_len, 0);
   if (max_context_len == 0 || sum_context_len * 10 < (int64_t)batch * max_context_len * 9)
     return automatic;
-  // Near-uniform rows: one round of the workgroups resident at once (4 per CU): at batch 32,
-  // 8 kv heads, 4096 tokens that is 1024-token splits (measured 97.4 us against 100.1 for
-  // 2048 and 102-103 for the automatic 320; 4096: 131.9).
+  // Near-uniform rows.  When whole rows fill the CUs in rounds that are at least 90% full,
+  // one split per row: the launch then runs one 16-wave workgroup per (row, kv head, head
+  // group), a whole CU each, with no partials and no merge launch (batch 32, 8 kv heads,
+  // 4096 tokens: 90.3-91.5 us against 94.1-94.5 for 1024-token splits).
   const long base = decode_base_blocks(batch, head_num, kv_head_num);
-  long per_row = (long)device_cus() * 4 / base;
+  const long cus = device_cus();
+  const long rounds = (base + cus - 1) / cus;
+  if (base >= cus && base * 10 >= rounds * cus * 9) return round_up(max_context_len, 64);
+  // Otherwise one round of the 4-wave workgroups resident at once (4 per CU): at batch 32,
+  // 8 kv heads, 4096 tokens that would be 1024-token splits (97.4 us against 100.1 for
+  // 2048 and 102-103 for the automatic 320).
+  long per_row = cus * 4 / base;
   if (per_row < 1) per_row = 1;
   int st = round_up((max_context_len + per_row - 1) / per_row, 64);
   while (n_splits(max_context_len, st) > kMaxSplits) st *= 2;

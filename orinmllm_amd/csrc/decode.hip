@@ -37,6 +37,10 @@ namespace {
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kMaxCombineSplits = 1024;  // the host sizes splits so a row has at most this many
+// Whole-row mode: one 16-wave workgroup (a whole CU at 128 VGPRs) per (row, kv head, head
+// group), no partials.  Its LDS merge holds kWideWaves * G * D floats.
+constexpr int kWideWaves = 16;
+constexpr int kWideMaxGD = 1024;
 
 template <typename T, int D>
 struct DecodeShape {
@@ -165,8 +169,8 @@ __device__ __forceinline__ int row_len(const DecodeArgs& a, int row) {
   return row_len_raw(a, row);
 }
 
-template <typename T, int D, int G, bool PAGED>
-__global__ void __launch_bounds__(kDecodeThreads)
+template <typename T, int D, int G, bool PAGED, int NW>
+__global__ void __launch_bounds__(NW * kWave)
 decode_split_kernel(DecodeArgs a) {
   using S = DecodeShape<T, D>;
   constexpr int NV = S::NV, VEC = S::VEC, STEPS = S::STEPS, TILE = S::TILE, EPL = S::EPL;
@@ -192,13 +196,13 @@ decode_split_kernel(DecodeArgs a) {
   T* out = reinterpret_cast<T*>(a.o) + (long)row * a.o_row_stride;
   if (len > a.len_cap) {  // longer than the launch covers: NaN output
     if (split == 0)
-      for (int i = threadIdx.x; i < G * D; i += kDecodeThreads)
+      for (int i = threadIdx.x; i < G * D; i += NW * kWave)
         out[(long)(h0 + i / D) * a.o_head_stride + i % D] = from_f32<T>(__builtin_nanf(""));
     return;
   }
   if (len <= 0) {  // empty row: output zeros
     if (split == 0)
-      for (int i = threadIdx.x; i < G * D; i += kDecodeThreads)
+      for (int i = threadIdx.x; i < G * D; i += NW * kWave)
         out[(long)(h0 + i / D) * a.o_head_stride + i % D] = from_f32<T>(0.f);
     return;
   }
@@ -303,7 +307,7 @@ decode_split_kernel(DecodeArgs a) {
     load_k(kc, t0, blk);
     load_v(vr, t0, blk);
     while (true) {
-      const int tn = t0 + kDecodeWaves * TILE;
+      const int tn = t0 + NW * TILE;
       const bool more = tn < s1;
       if (more) k_blocks(nblk, tn);  // in flight while this tile's scores are computed
 
@@ -397,8 +401,8 @@ decode_split_kernel(DecodeArgs a) {
   for (int g = 0; g < G; ++g) l[g] = sum_across_groups8(l[g]);
 
   // Merge the 4 waves through LDS.
-  __shared__ float s_acc[kDecodeWaves][G][D];
-  __shared__ float s_ml[kDecodeWaves][G][2];
+  __shared__ float s_acc[NW][G][D];
+  __shared__ float s_ml[NW][G][2];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -413,14 +417,14 @@ decode_split_kernel(DecodeArgs a) {
   __syncthreads();
 
   const bool direct = (nsplit == 1);
-  for (int i = threadIdx.x; i < G * D; i += kDecodeThreads) {
+  for (int i = threadIdx.x; i < G * D; i += NW * kWave) {
     const int g = i / D, dd = i % D;
     float M = s_ml[0][g][0];
 #pragma unroll
-    for (int w = 1; w < kDecodeWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_ml[w][g][0]);
     float L = 0.f, o = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float f = fast_exp2(s_ml[w][g][0] - M);
       L += f * s_ml[w][g][1];
       o += f * s_acc[w][g][dd];
@@ -514,11 +518,22 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
 template <typename T, int D, int G>
 hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_rows * a.Hkv * (a.kv_mul / G) * a.max_splits;
+  if constexpr (sizeof(T) == 2 && G * D <= kWideMaxGD) {
+    if (a.wide && a.max_splits == 1) {
+      if (a.block_table)
+        hipLaunchKernelGGL((decode_split_kernel<T, D, G, true, kWideWaves>), dim3((unsigned)blocks),
+                           dim3(kWideWaves * kWave), 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_split_kernel<T, D, G, false, kWideWaves>),
+                           dim3((unsigned)blocks), dim3(kWideWaves * kWave), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   if (a.block_table)
-    hipLaunchKernelGGL((decode_split_kernel<T, D, G, true>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, true, kDecodeWaves>), dim3((unsigned)blocks),
                        dim3(kDecodeThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<T, D, G, false>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((decode_split_kernel<T, D, G, false, kDecodeWaves>), dim3((unsigned)blocks),
                        dim3(kDecodeThreads), 0, stream, a);
   if (a.max_splits > 1)
     hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.n_rows * a.Hq)), dim3(64),

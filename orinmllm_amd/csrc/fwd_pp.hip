@@ -54,7 +54,8 @@ constexpr int PTILE_BYTES = PBN * PD * 2;              // 16 KB
 constexpr int PKREGION = PSTAGES * PTILE_BYTES;        // K ring, then V ring
 constexpr int PLDS_BYTES = 2 * PKREGION;               // 96 KB
 constexpr int kXcdsPP = 8;
-constexpr float kLazyRescalePP = 8.0f;
+// A lane's 32 weights of one tile may sum to at most this before the row maximum is raised.
+constexpr float kTileSumMax = 256.0f;
 #ifndef PP_PF
 #define PP_PF 3
 #endif
@@ -500,8 +501,14 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
   f32x16 sacc[2];
   u32x4 pf[4];
-  float m_use = -INFINITY, l_run = 0.f;
+  // Running row maximum m (raw score units) and its negation in every accumulator slot:
+  // the QK^T MFMA chains start from `negm`, so S' = s - m leaves the matrix pipe and the
+  // softmax needs no subtraction per score.
   const float c = a.scale_log2;
+  float m_use = 0.f, l_run = 0.f;
+  f32x16 negm;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
 
   auto active = [&](int t) __attribute__((always_inline)) {
     return !CAUSAL || (t_lo + t) * PBN <= wpos0 + 31;
@@ -521,10 +528,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 
   // S(0)^T = K(0) . Q^T (K(0) is in ring slot 0).
   auto qk0 = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+    sacc[0] = negm;
+    sacc[1] = negm;
     constexpr int NQK = 2 * QS;
     u32x4 fr[PF + 1];
 #pragma unroll
@@ -547,10 +552,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     constexpr PhaseOrder<NQK, NPV> order{};
     constexpr int sl_off = decltype(slot_tag)::value * PTILE_BYTES;
     if (QK) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+      sacc[0] = negm;
+      sacc[1] = negm;
     }
     // MFMA i: QK step j = (kt = j & 1, slice j >> 1) or PV step n = (chunk n / DT, d-tile
     // n % DT), in the order of PhaseOrder.
@@ -576,7 +579,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     sgb_seq<NQK, NPV, 0>();
   };
 
-  // Softmax of S(t) into P(t) (packed 16-bit), online max / sum with lazy rescale.
+  // Softmax of S'(t) into P(t) (packed 16-bit).  Fast path: P = 2^(c*S') with the
+  // running maximum m left as it is, valid while every weight stays at most 2^8 (checked
+  // through each lane's sum of its 32 weights); otherwise (and on the first tile, where m
+  // is not yet set) the row maximum is taken, m raised to it, O and l rescaled and P
+  // recomputed.  The weights then never exceed 2^8 and the normaliser never underflows.
   auto softmax = [&](int t) __attribute__((always_inline)) {
     const int t0 = (t_lo + t) * PBN;
     const bool need_mask = CAUSAL ? (t0 + PBN - 1 > wpos0) : (t0 + PBN > kv_end);
@@ -592,35 +599,49 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
           sacc[kt][r] = cr > rel ? -INFINITY : sacc[kt][r];
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, partner32(mx)) * c;
-    const float m_old = m_use;
-    const float m_new = (mx > m_old + kLazyRescalePP) ? mx : m_old;
-    m_use = m_new;
-    if (__builtin_amdgcn_ballot_w64(m_new != m_old)) {
-      const float alpha = fast_exp2(m_old - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < DT; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
-    }
-    float ls = l_run;
+    float ls = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -m_new));
-        const float p1 = fast_exp2(__builtin_fmaf(sacc[kt][r + 1], c, -m_new));
-        const uint32_t pk = pack2<T>(p0, p1);
+        const uint32_t pk =
+            pack2<T>(fast_exp2(sacc[kt][r] * c), fast_exp2(sacc[kt][r + 1] * c));
         pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
         ls = sum_pair<T>(pk, ls);
       }
-    l_run = ls;
+    const bool first = t == 0;
+    if (__builtin_amdgcn_ballot_w64(first || !(ls <= kTileSumMax))) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+      mx = fmaxf(mx, partner32(mx));
+      // raise m by `up`: to the row maximum on the first tile, else only upwards
+      const float up = first ? (mx > -INFINITY ? mx : 0.f) : fmaxf(mx, 0.f);
+      m_use += up;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) negm[r] = -m_use;
+      if (!first && __builtin_amdgcn_ballot_w64(up != 0.f)) {
+        const float alpha = fast_exp2(-up * c);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+      }
+      ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const uint32_t pk =
+              pack2<T>(fast_exp2((sacc[kt][r] - up) * c), fast_exp2((sacc[kt][r + 1] - up) * c));
+          pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
+          ls = sum_pair<T>(pk, ls);
+        }
+    }
+    l_run += ls;
   };
 
   // Step bookkeeping shared by both groups: at the start of even step k >= 2 issue
@@ -723,7 +744,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
         }
       if (hf == 0) {
         float* ml = a.ws + pp_ml_offset(a, D, sizeof(PT)) + row * 2;
-        ml[0] = m_use;
+        ml[0] = m_use * a.scale_log2;
         ml[1] = l_tot;
       }
     }

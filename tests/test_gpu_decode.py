@@ -169,7 +169,8 @@ def test_paged_equals_contiguous_bit_exact(kind, layout):
     q = quantize(normal(rng, (B, Hq, d)), kind)
     lens_d = torch.from_numpy(lens).cuda()
     maxlen = int(lens.max())
-    for split in [0, 64, 256]:
+    # 4096: one split per row (16-bit K/V then run the whole-row 16-wave workgroups)
+    for split in [0, 64, 256, 4096]:
         oc = torch.zeros(B, Hq, d, device="cuda", dtype=TORCH[kind])
         op = torch.zeros_like(oc)
         K.batched_decode_cu(dev(q, kind), dev(kc, kind), dev(vc, kind), oc, lens_d, maxlen, Hkv,
