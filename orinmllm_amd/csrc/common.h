@@ -36,6 +36,20 @@ __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
 
+// bf16 -> fp16 on 16-bit pairs.  Exact for values in fp16's normal range (bf16 carries 8
+// significant bits, fp16 11).  bf16 attention keeps its softmax weights in fp16 (2^-12
+// rounding instead of bf16's 2^-9, which on a near-cancelling output is as large as the
+// output tolerance) and converts V to fp16 for the weighted sum.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t x) {
+  const float lo = __builtin_bit_cast(float, x << 16);
+  const float hi = __builtin_bit_cast(float, x & 0xffff0000u);
+  return __builtin_bit_cast(uint32_t, f16x2{(f16)lo, (f16)hi});
+}
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(const u32x4& x) {
+  return u32x4{bf16x2_to_f16x2(x[0]), bf16x2_to_f16x2(x[1]), bf16x2_to_f16x2(x[2]),
+               bf16x2_to_f16x2(x[3])};
+}
+
 // Hardware base-2 exponential (v_exp_f32).  exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -27,6 +27,8 @@
 //  * Token addresses come from a contiguous map (optionally per varlen segment) or a
 //    paged block table.  The arithmetic does not depend on the map, so paged and
 //    contiguous decode of the same KV are bit-identical.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -38,9 +40,13 @@ constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kMaxCombineSplits = 1024;  // the host sizes splits so a row has at most this many
 // Whole-row mode: one 16-wave workgroup (a whole CU at 128 VGPRs) per (row, kv head, head
-// group), no partials.  Its LDS merge holds kWideWaves * G * D floats.
+// group), no partials.  Only the shapes whose loop fits 128 VGPRs without spilling use it
+// (16-bit K/V, head size 128 with up to 4 heads per group, 64 with up to 3).
 constexpr int kWideWaves = 16;
-constexpr int kWideMaxGD = 1024;
+template <typename T, int D, int G>
+constexpr bool wide_fits() {
+  return sizeof(T) == 2 && ((D == 128 && G <= 4) || (D == 64 && G <= 3));
+}
 
 template <typename T, int D>
 struct DecodeShape {
@@ -352,24 +358,28 @@ decode_split_kernel(DecodeArgs a) {
       // broadcast with v_readlane into scalar registers.
       if constexpr (sizeof(T) == 2) {
         // 16-bit K/V: tokens 8(2u)+r and 8(2u+1)+r share one packed weight pair, so one
-        // v_dot2 does two tokens.  The weights are rounded to T (as P is in the MFMA
-        // prefill); the normaliser l keeps the fp32 weights.
-        typedef T T2 __attribute__((ext_vector_type(2)));
+        // v_dot2 does two tokens.  The weights are rounded to fp16 (as P is in the MFMA
+        // prefill; bf16 V pairs are converted to fp16); the normaliser l keeps the fp32
+        // weights.
 #pragma unroll
         for (int u = 0; u < STEPS / 2; ++u) {
           uint32_t pw[G];
 #pragma unroll
           for (int g = 0; g < G; ++g)
-            pw[g] = __builtin_bit_cast(uint32_t, T2{(T)sc[2 * u][g], (T)sc[2 * u + 1][g]});
+            pw[g] = __builtin_bit_cast(uint32_t, f16x2{(f16)sc[2 * u][g], (f16)sc[2 * u + 1][g]});
 #pragma unroll
           for (int r = 0; r < 8; ++r) {
             uint32_t vp[EPL];
             pair_rows<EPL>(vr[16 * u + r], vr[16 * u + 8 + r], vp);
+            if constexpr (!std::is_same<T, f16>::value) {
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) vp[e] = bf16x2_to_f16x2(vp[e]);
+            }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
               const uint32_t p2 = __builtin_amdgcn_readlane(pw[g], r * 8);
 #pragma unroll
-              for (int e = 0; e < EPL; ++e) acc[g][e] = dot2<T>(p2, vp[e], acc[g][e]);
+              for (int e = 0; e < EPL; ++e) acc[g][e] = dot2<f16>(p2, vp[e], acc[g][e]);
             }
           }
         }
@@ -518,7 +528,7 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
 template <typename T, int D, int G>
 hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_rows * a.Hkv * (a.kv_mul / G) * a.max_splits;
-  if constexpr (sizeof(T) == 2 && G * D <= kWideMaxGD) {
+  if constexpr (wide_fits<T, D, G>()) {
     if (a.wide && a.max_splits == 1) {
       if (a.block_table)
         hipLaunchKernelGGL((decode_split_kernel<T, D, G, true, kWideWaves>), dim3((unsigned)blocks),

@@ -38,6 +38,8 @@
 // Scheduling: causal blocks start longest-first.  When the kv heads split evenly over
 // the 8 XCDs, block i (dispatched to XCD i % 8) serves a query head of kv head
 // i % 8 + 8k, so a kv head's K/V stay in one XCD's L2.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -200,14 +202,19 @@ struct TileStage {
       if (u < S::VU_TOTAL) {
         const int kb4 = u % (BN / 4), db = u / (BN / 4);
         const int pos = vt_pos(kb4 * 4);
-        // 4 keys x 8 dims -> 8 rows (dims) of 4 consecutive keys.
+        // 4 keys x 8 dims -> 8 rows (dims) of 4 consecutive keys; bf16 V is stored as
+        // fp16 (the PV product runs on fp16 MFMAs with fp16 weights).
+        u32x4 vv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vv[r] = std::is_same<T, f16>::value ? v[i][r] : bf16x8_to_f16x8(v[i][r]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           // element e of keys (0,1) and (2,3): one v_perm_b32 per packed pair
           const int w = e >> 1;
           const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          u32x2 pk = {__builtin_amdgcn_perm(v[i][1][w], v[i][0][w], sel),
-                      __builtin_amdgcn_perm(v[i][3][w], v[i][2][w], sel)};
+          u32x2 pk = {__builtin_amdgcn_perm(vv[1][w], vv[0][w], sel),
+                      __builtin_amdgcn_perm(vv[3][w], vv[2][w], sel)};
           *reinterpret_cast<u32x2*>(sV + (db * 8 + e) * S::SV + pos) = pk;
         }
       }
@@ -374,9 +381,9 @@ __global__ void __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) fwd_kernel(FwdArgs a
         for (int r = 0; r < 16; r += 2) {
           const float p0 = fast_exp2(__builtin_fmaf(sacc[kt][r], c, -m_new));
           const float p1 = fast_exp2(__builtin_fmaf(sacc[kt][r + 1], c, -m_new));
-          const uint32_t pk = pack2<T>(p0, p1);
+          const uint32_t pk = pack2<f16>(p0, p1);
           pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
-          ls = sum_pair<T>(pk, ls);
+          ls = sum_pair<f16>(pk, ls);
         }
       l_run = ls;
 
@@ -393,7 +400,7 @@ __global__ void __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) fwd_kernel(FwdArgs a
           vf[(n + 1) & 1] = *reinterpret_cast<const u32x4*>(sV + (t1 * 32 + lq) * S::SV +
                                                             16 * ck1 + 8 * hf);
         }
-        oacc[t] = mfma32<T>(vf[n & 1], pf[ck], oacc[t]);
+        oacc[t] = mfma32<f16>(vf[n & 1], pf[ck], oacc[t]);
       }
     }
 

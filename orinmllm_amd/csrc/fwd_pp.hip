@@ -49,10 +49,13 @@ constexpr int PBN = 64;            // keys per tile
 constexpr int PNW = 8;             // waves per workgroup
 constexpr int PBM = 32 * PNW;      // query rows per workgroup
 constexpr int PTHREADS = PNW * kWave;
-constexpr int PSTAGES = 3;         // LDS ring depth
 constexpr int PTILE_BYTES = PBN * PD * 2;              // 16 KB
-constexpr int PKREGION = PSTAGES * PTILE_BYTES;        // K ring, then V ring
-constexpr int PLDS_BYTES = 2 * PKREGION;               // 96 KB
+// LDS ring depth: 3 stages for fp16; 4 for bf16, whose V tiles are converted to fp16 in
+// LDS one step before the MFMA phases read them.  K ring, then V ring.
+template <typename T>
+constexpr int pp_stages() { return std::is_same<T, f16>::value ? 3 : 4; }
+template <typename T>
+constexpr int pp_lds_bytes() { return 2 * pp_stages<T>() * PTILE_BYTES; }  // 96 / 128 KB
 constexpr int kXcdsPP = 8;
 // A lane's 32 weights of one tile may sum to at most this before the row maximum is raised.
 constexpr float kTileSumMax = 256.0f;
@@ -110,6 +113,17 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait for the K/V transfers of all but the `younger` most recent stages (four transfers
+// per wave and stage).
+__device__ __forceinline__ void wait_stage(int younger) {
+  switch (younger) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<4>(); break;
+    case 2: wait_vmcnt<8>(); break;
+    default: wait_vmcnt<12>(); break;
+  }
 }
 
 // Workgroup barrier that the scheduler may not move any instruction across.
@@ -328,6 +342,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   constexpr int QS = (D + 15) / 16;  // 16-wide slices of the QK contraction (zero-padded)
   constexpr int DT = (D + 31) / 32;  // 32-wide output tiles of O^T
   constexpr int NCH = D / 8;         // valid 16-byte chunks of a K / V row
+  // bf16: P stays fp16 (2^-12 rounding; bf16's 2^-9 would be as large as the output's),
+  // so the PV product runs on fp16 MFMAs over V tiles converted to fp16 in LDS.
+  constexpr bool kConvV = !std::is_same<T, f16>::value;
+  constexpr int PSTAGES = pp_stages<T>();
+  constexpr int PKREGION = PSTAGES * PTILE_BYTES;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -483,15 +502,15 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     }
   }
 
-  // Stages 0..2 up front; wait for stage 0 (younger stages may stay in flight).
+  // Stages 0 .. PSTAGES-1 up front; wait for stage 0 (younger stages may stay in flight).
   issue_stage(0);
-  if (n_tiles >= 1) issue_stage(1);
-  if (n_tiles >= 2) issue_stage(2);
+#pragma unroll
+  for (int u = 1; u < PSTAGES; ++u)
+    if (n_tiles >= u) issue_stage(u);
   // The fused Q producer works while the first stages are in flight.
   if constexpr (FQ && CAUSAL && (D == 64 || D == 128))
     fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
-  if (n_tiles >= 2) wait_vmcnt<8>();
-  else wait_vmcnt<4>();
+  wait_stage(min(n_tiles, PSTAGES - 1));
   step_barrier();
 
   f32x16 oacc[DT];
@@ -572,7 +591,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
         sacc[j & 1] = mfma32<T>(fr[i % (PF + 1)], qf[j >> 1], sacc[j & 1]);
       } else {
         const int n = order.idx[i];
-        oacc[n % DT] = mfma32<T>(fr[i % (PF + 1)], pf[n / DT], oacc[n % DT]);
+        oacc[n % DT] = mfma32<f16>(fr[i % (PF + 1)], pf[n / DT], oacc[n % DT]);
       }
     }
     sgb_head<NQK, NPV, 0>();
@@ -605,9 +624,9 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const uint32_t pk =
-            pack2<T>(fast_exp2(sacc[kt][r] * c), fast_exp2(sacc[kt][r + 1] * c));
+            pack2<f16>(fast_exp2(sacc[kt][r] * c), fast_exp2(sacc[kt][r + 1] * c));
         pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
-        ls = sum_pair<T>(pk, ls);
+        ls = sum_pair<f16>(pk, ls);
       }
     const bool first = t == 0;
     if (__builtin_amdgcn_ballot_w64(first || !(ls <= kTileSumMax))) {
@@ -636,26 +655,53 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
           const uint32_t pk =
-              pack2<T>(fast_exp2((sacc[kt][r] - up) * c), fast_exp2((sacc[kt][r + 1] - up) * c));
+              pack2<f16>(fast_exp2((sacc[kt][r] - up) * c), fast_exp2((sacc[kt][r + 1] - up) * c));
           pf[kt * 2 + (r >> 3)][(r & 7) >> 1] = pk;
-          ls = sum_pair<T>(pk, ls);
+          ls = sum_pair<f16>(pk, ls);
         }
     }
     l_run += ls;
   };
 
-  // Step bookkeeping shared by both groups: at the start of even step k >= 2 issue
-  // stage k/2 + 2; at the end of odd step k wait for stage (k+1)/2 (the next stage may
-  // stay in flight) and publish it with the barrier.
+  // Step bookkeeping shared by both groups.  Group 0 runs M(t) at step 2t+2 and softmax(t)
+  // at step 2t+1, group 1 one step later; M(t) reads stage t+1.
+  //  fp16: stage u is published by the barrier that ends step 2u-1 and issued at the
+  //        start of step 2u-4 (three stages).
+  //  bf16: stage u is published one step earlier (end of step 2u-2); group 0 converts its
+  //        V tile to fp16 in place during step 2u-1 (its softmax step), the barrier ending
+  //        that step publishes the result; it is issued at the start of step 2u-6 (four
+  //        stages: the slot's previous stage was last read by group 1's M(u-5) at step
+  //        2u-7).
   const int last_step = 2 * n_tiles + 1;
   auto step_begin = [&](int k) __attribute__((always_inline)) {
     if (!(k & 1) && k >= 2) {
-      const int u = k / 2 + 2;
+      const int u = k / 2 + PSTAGES - 1;
       if (u <= n_tiles) issue_stage(u);
     }
   };
+  auto convert_v = [&](int u) __attribute__((always_inline)) {
+    // wave w converts bytes [2048 w, 2048 w + 2048) of the stage's V tile
+    lds_ptr base = lds0 + PKREGION + (u % PSTAGES) * PTILE_BYTES + wave * 2048 + lane * 16;
+    u32x4 x[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) x[j] = lds_read128(base, j * 1024);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+          const_cast<__attribute__((address_space(3))) char*>(base + j * 1024)) =
+          bf16x8_to_f16x8(x[j]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the writes land before the barrier
+  };
   auto step_end = [&](int k) __attribute__((always_inline)) {
-    if (k & 1) {
+    if constexpr (kConvV) {
+      if (!(k & 1)) {
+        const int u = k / 2 + 1;
+        if (u <= n_tiles) wait_stage(min(n_tiles, k / 2 + PSTAGES - 1) - u);
+      } else {
+        const int u = (k + 1) / 2;
+        if (u <= n_tiles) convert_v(u);
+      }
+    } else if (k & 1) {
       const int u = (k + 1) / 2;
       if (u + 1 <= n_tiles) wait_vmcnt<4>();
       else wait_vmcnt<0>();
@@ -677,8 +723,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   softmax(0);
   step_end(k);
   ++k;
-  // Tile t's MFMA phase reads ring slot (t+1) % 3; the loop is unrolled by three so
-  // every LDS offset is a compile-time constant.  Tiles before the last one always run
+  // Tile t's MFMA phase reads ring slot (t+1) % PSTAGES; the loop is unrolled by
+  // PSTAGES so every LDS offset is a compile-time constant.  Tiles before the last one always run
   // the QK product of the next tile, also for a wave whose queries all precede it: one
   // MFMA-phase shape inside the loop keeps the accumulators in fixed registers.
   auto tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
@@ -694,10 +740,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     ++k;
   };
   const int n_loop = n_tiles - 1;
-  for (int t = 0; t < n_loop; t += 3) {
+  for (int t = 0; t < n_loop; t += PSTAGES) {
     tile(t, std::integral_constant<int, 1>{});
     if (t + 1 < n_loop) tile(t + 1, std::integral_constant<int, 2>{});
-    if (t + 2 < n_loop) tile(t + 2, std::integral_constant<int, 0>{});
+    if (t + 2 < n_loop) tile(t + 2, std::integral_constant<int, 3 % PSTAGES>{});
+    if (PSTAGES > 3 && t + 3 < n_loop) tile(t + 3, std::integral_constant<int, 4 % PSTAGES>{});
   }
   {  // last tile: PV only
     const int t = n_loop;
@@ -707,7 +754,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       switch ((t + 1) % PSTAGES) {
         case 0: mphase(std::integral_constant<int, 0>{}, std::false_type{}); break;
         case 1: mphase(std::integral_constant<int, 1>{}, std::false_type{}); break;
-        default: mphase(std::integral_constant<int, 2>{}, std::false_type{}); break;
+        case 2: mphase(std::integral_constant<int, 2>{}, std::false_type{}); break;
+        default: mphase(std::integral_constant<int, 3 % PSTAGES>{}, std::false_type{}); break;
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -853,16 +901,16 @@ hipError_t launch_pp_d(const FwdArgs& a, hipStream_t stream) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev >= 64 || !(__atomic_load_n(&configured[fq], __ATOMIC_ACQUIRE) & (1ull << dev))) {
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, PLDS_BYTES);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, pp_lds_bytes<T>());
     if (e != hipSuccess) return e;
     if (dev < 64) __atomic_fetch_or(&configured[fq], 1ull << dev, __ATOMIC_RELEASE);
   }
   if (fq)
     hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D, kFusable>), dim3((unsigned)blocks),
-                       dim3(PTHREADS), PLDS_BYTES, stream, a);
+                       dim3(PTHREADS), pp_lds_bytes<T>(), stream, a);
   else
     hipLaunchKernelGGL((fwd_pp_kernel<T, CAUSAL, D, false>), dim3((unsigned)blocks),
-                       dim3(PTHREADS), PLDS_BYTES, stream, a);
+                       dim3(PTHREADS), pp_lds_bytes<T>(), stream, a);
   if (CAUSAL && a.key_chunk_tiles > 0) {
     const int nqb = (a.n_q + PBM - 1) / PBM;
     hipLaunchKernelGGL((fwd_pp_merge<T, D>), dim3((unsigned)(nqb * a.Hq * (PBM / kMergeRows))),

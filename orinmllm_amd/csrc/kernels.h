@@ -30,7 +30,7 @@ struct DecodeArgs {
   long o_row_stride, o_head_stride;
   float* ws;  // [n_rows, Hq, max_splits, head_size + 2] fp32 partials (unused if max_splits == 1)
   int max_splits, split_tokens;
-  int wide;  // one split per row: 16-wave workgroups (16-bit K/V, G * head_size <= 1024)
+  int wide;  // one split per row: 16-wave workgroups where the shape fits (decode.hip)
   int n_rows, Hq, Hkv, kv_mul, head_size;
   float scale_log2;  // softmax scale * log2(e)
 };
