@@ -13,13 +13,17 @@
 // time:
 //   MFMA phase M(t):  S(t+1)^T = K(t+1) . Q^T     (16 v_mfma_f32_32x32x16)
 //                     O^T     += V(t)^T . P(t)^T  (16 v_mfma_f32_32x32x16)
-//   softmax phase V(t): mask, row max, lazy rescale, exp2, P(t+1) packed to 16 bits.
+//   softmax phase V(t): mask, exp2 of S' = s - m (the QK^T accumulators start at -m),
+//                       P packed to fp16; the row maximum m is raised (and O, l
+//                       rescaled) only when a tile's weights would exceed 2^8.
 // Group 0 runs M at even steps, group 1 at odd steps.
 //
 // K/V tiles (64 keys) reach LDS through global_load_lds_dwordx4 (no register staging),
-// in a ring of three stages; stage u holds K(u) and V(u-1) and is read in steps 2u and
-// 2u+1.  Every wave moves 1/8 of a stage (four 1 KB transfers) and waits for its own
-// transfers with vmcnt before the barrier that publishes them.
+// in a ring of three stages (four for bf16); stage u holds K(u) and V(u-1) and is read in
+// steps 2u and 2u+1.  Every wave moves 1/8 of a stage (four 1 KB transfers) and waits for
+// its own transfers with vmcnt before the barrier that publishes them.  For bf16 inputs
+// the V tile of each stage is converted to fp16 in LDS before it is read, so P and the PV
+// MFMAs are fp16 (bf16's 2^-9 rounding of P would be as large as the output tolerance).
 //   K rows are stored row-major with 16-byte chunk c of row r at chunk c ^ (r & 15):
 //   the K fragment reads (one row per lane, same chunk) are then conflict-free.
 //   V rows are stored row-major with chunk c of row r at chunk c ^ 4(r & 3) and read
@@ -667,11 +671,11 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // at step 2t+1, group 1 one step later; M(t) reads stage t+1.
   //  fp16: stage u is published by the barrier that ends step 2u-1 and issued at the
   //        start of step 2u-4 (three stages).
-  //  bf16: stage u is published one step earlier (end of step 2u-2); group 0 converts its
-  //        V tile to fp16 in place during step 2u-1 (its softmax step), the barrier ending
-  //        that step publishes the result; it is issued at the start of step 2u-6 (four
-  //        stages: the slot's previous stage was last read by group 1's M(u-5) at step
-  //        2u-7).
+  //  bf16: stage u is published one step earlier (end of step 2u-2); at the end of step
+  //        2u-1 every wave converts 1/8 of its V tile to fp16 in place (no phase reads
+  //        stage u in that step), and the barrier ending that step publishes the result;
+  //        it is issued at the start of step 2u-6 (four stages: the slot's previous stage
+  //        was last read by group 1's M(u-5) at step 2u-7).
   const int last_step = 2 * n_tiles + 1;
   auto step_begin = [&](int k) __attribute__((always_inline)) {
     if (!(k & 1) && k >= 2) {
