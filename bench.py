@@ -328,7 +328,7 @@ def time_fused_pipeline(K, dtype, gen, reps=50):
     K.sin_cos_cache_calc_cu(d, S, sn, cs, 1e6)
     kc = torch.empty(1, S, Hkv * d, device=dev, dtype=dtype)
     vc = torch.empty_like(kc)
-    qw = torch.empty_like(q)
+    qw = q.clone()  # the producer normalises and rotates it in place
     o = torch.empty_like(q)
     stream = torch.cuda.current_stream()
     prod_qkv = lambda: K.qk_norm_rope_cu(qw, k, v, wq, wk, sn, cs, kc, vc, 0, S, 0, S, Hq, Hkv, d)
