@@ -59,3 +59,21 @@ def test_paged_decode_sweep(i, kind, B, Hq, Hkv, d, bs, layout, split):
         assert_fp32_close(got[live], ref, d, what=f"sweep case {i}")
     else:
         assert_lowp_close(got[live], ref, what=f"sweep case {i}")
+    # The same batch with one split per row: 16-bit K/V run the whole-row (16-wave)
+    # workgroups where the shape allows; still bit-equal between paged and contiguous.
+    whole = (maxlen + 63) // 64 * 64
+    op1 = torch.full((B, Hq, d), 7.0, device="cuda", dtype=TORCH[kind])
+    oc1 = torch.zeros_like(op1)
+    K.paged_decode_cu(dev(q, kind), dev(kpl, kind), dev(vpl, kind), op1,
+                      torch.from_numpy(bt).cuda(), lens_d, maxlen, split_tokens=whole,
+                      layout=layout)
+    K.batched_decode_cu(dev(q, kind), dev(kc, kind), dev(vc, kind), oc1, lens_d, maxlen, Hkv,
+                        split_tokens=whole)
+    torch.cuda.synchronize()
+    assert torch.equal(op1, oc1), f"sweep case {i}: whole-row paged != contiguous"
+    got1 = host(op1)
+    assert np.all(got1[empty] == 0.0), f"sweep case {i}: whole-row empty rows"
+    if kind == "fp32":
+        assert_fp32_close(got1[live], ref, d, what=f"sweep case {i} whole-row")
+    else:
+        assert_lowp_close(got1[live], ref, what=f"sweep case {i} whole-row")
