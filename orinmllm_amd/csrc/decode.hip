@@ -39,6 +39,8 @@ namespace {
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kMaxCombineSplits = 1024;  // the host sizes splits so a row has at most this many
+// A wave keeps its running maximum while every weight stays at most 2^kDecodeLazyLog2.
+constexpr float kDecodeLazyLog2 = 8.0f;
 // Whole-row mode: one 16-wave workgroup (a whole CU at 128 VGPRs) per (row, kv head, head
 // group), no partials.  Only the shapes whose loop fits 128 VGPRs without spilling use it
 // (16-bit K/V, head size 128 with up to 4 heads per group, 64 with up to 3).
@@ -332,28 +334,39 @@ decode_split_kernel(DecodeArgs a) {
       }
       if (more) load_k(kc, tn, nblk);
 
-      float alpha[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float tm = sc[0][g];
-#pragma unroll
-        for (int s = 1; s < STEPS; ++s) tm = fmaxf(tm, sc[s][g]);
-        tm = max_across_groups8(tm);
-        const float mn = fmaxf(m[g], tm);
-        alpha[g] = fast_exp2(m[g] - mn);
-        m[g] = mn;
-        float ls = 0.f;
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-          sc[s][g] = fast_exp2(sc[s][g] - mn);
-          ls += sc[s][g];
-        }
-        l[g] = l[g] * alpha[g] + ls;
-      }
+      // Weights 2^(s - m) against the wave's running maximum m, which is raised (and acc, l
+      // rescaled) only when a weight would exceed 2^8, and on the wave's first tile (m =
+      // -inf): the exact tile maximum and its lane-group reduction are skipped otherwise.
+      bool raise = false;
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha[g];
+        for (int s = 0; s < STEPS; ++s) raise |= sc[s][g] - m[g] > kDecodeLazyLog2;
+      if (__builtin_amdgcn_ballot_w64(raise)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float tm = sc[0][g];
+#pragma unroll
+          for (int s = 1; s < STEPS; ++s) tm = fmaxf(tm, sc[s][g]);
+          tm = max_across_groups8(tm);
+          const float mn = fmaxf(m[g], tm);
+          const float alpha = fast_exp2(m[g] - mn);
+          m[g] = mn;
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float ls = 0.f;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+          sc[s][g] = fast_exp2(sc[s][g] - m[g]);
+          ls += sc[s][g];
+        }
+        l[g] += ls;
+      }
       // Token j = 8s + r of the tile has its weights in lane group r (lane 8r); they are
       // broadcast with v_readlane into scalar registers.
       if constexpr (sizeof(T) == 2) {
