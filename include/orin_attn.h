@@ -235,10 +235,13 @@ int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t k
  * rows' context lengths) the caller knows on the host -- a serving loop keeps it; no
  * reference counterpart.  When every row is close to max_context_len (sum >= 0.9 * batch *
  * max_context_len) the launch gets one split per row when the (row, kv head) units fill
- * the CUs in rounds at least 90% full (16-bit K/V then run one whole-CU workgroup per unit
- * and no merge), else a few long splits per row (one round of the workgroups the device
- * holds at once); both stream faster than the automatic choice.  Otherwise it returns
- * the automatic choice.  Pass the result as split_tokens (and to
+ * the CUs in rounds at least 90% full, else a few long splits per row (one round of the
+ * workgroups the device holds at once); both stream faster than the automatic choice.
+ * Otherwise it returns the automatic choice.  A launch with one split per row runs one
+ * 16-wave (whole-CU) workgroup per (row, kv head, head group) and no merge when K/V are
+ * 16-bit and head_size is 128 with at most 4 query heads per kv head, or 64 with at most
+ * 3; other shapes run 4-wave workgroups, which a near-uniform batch of whole rows does not
+ * fill, so pass such callers' automatic split instead.  Pass the result as split_tokens (and to
  * orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid arguments.
  */
 int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,
