@@ -43,11 +43,13 @@ constexpr int kMaxCombineSplits = 1024;  // the host sizes splits so a row has a
 constexpr float kDecodeLazyLog2 = 8.0f;
 // Whole-row mode: one 16-wave workgroup (a whole CU at 128 VGPRs) per (row, kv head, head
 // group), no partials.  Only the shapes whose loop fits 128 VGPRs without spilling use it
-// (16-bit K/V, head size 128 with up to 4 heads per group, 64 with up to 3).
+// (16-bit K/V: head size 128 with up to 4 heads per group, 64 with up to 3; fp32: head
+// size 64 with 1 head per group).
 constexpr int kWideWaves = 16;
 template <typename T, int D, int G>
 constexpr bool wide_fits() {
-  return sizeof(T) == 2 && ((D == 128 && G <= 4) || (D == 64 && G <= 3));
+  if (sizeof(T) == 4) return D == 64 && G == 1;
+  return (D == 128 && G <= 4) || (D == 64 && G <= 3);
 }
 
 template <typename T, int D>
