@@ -240,7 +240,9 @@ int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t k
  * Otherwise it returns the automatic choice.  A launch with one split per row runs one
  * 16-wave (whole-CU) workgroup per (row, kv head, head group) and no merge when K/V are
  * 16-bit and head_size is 128 with at most 4 query heads per kv head, or 64 with at most
- * 3; other shapes run 4-wave workgroups, which a near-uniform batch of whole rows does not
+ * 3 (fp32: head_size 64, one query head per kv head); the same 16-wave workgroups (then
+ * followed by the merge) also run any split launch with no more workgroups than the
+ * device has CUs, e.g. batch 1.  Other shapes run 4-wave workgroups, which a near-uniform batch of whole rows does not
  * fill, so pass such callers' automatic split instead.  Pass the result as split_tokens (and to
  * orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid arguments.
  */

@@ -2,6 +2,8 @@
 // Argument checking, the per-call launch shape (split-KV sizing) and the
 // library-owned decode workspace live here; the kernels are in decode.hip and fwd.hip.
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include <mutex>
 #include <string>
@@ -146,6 +148,14 @@ int device_cus() {
   return cached;
 }
 
+bool wide_small_launches() {
+  static const bool on = [] {
+    const char* e = getenv("ORIN_DECODE_WIDE_SMALL");
+    return !(e && !strcmp(e, "0"));
+  }();
+  return on;
+}
+
 DecodeArgs decode_defaults() {
   DecodeArgs a = {};
   a.max_splits = 1;
@@ -170,7 +180,11 @@ int kuiper_decode_split(int head_num, int kv_head_num, int head_size, int max_le
 int run_decode(DecodeArgs& a, int dtype, int max_len, hipStream_t stream) {
   a.max_splits = n_splits(max_len, a.split_tokens);
   if (a.max_splits <= 1) a.max_splits = 1;
-  a.wide = a.max_splits == 1;
+  // 16-wave workgroups (where the shape fits) when each (row, kv head, head group) is one
+  // split, or when the launch has no more workgroups than the device has CUs: 4-wave
+  // workgroups would then leave most wave slots idle.
+  const long units = (long)a.n_rows * a.Hkv * (a.kv_mul / decode_heads_per_block(a.kv_mul));
+  a.wide = a.max_splits == 1 || (wide_small_launches() && units * a.max_splits <= device_cus());
   a.len_cap = max_len > 0 ? max_len : (1 << 30);
   return hip_status(launch_decode(a, dtype, stream));
 }

@@ -543,23 +543,24 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
 template <typename T, int D, int G>
 hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_rows * a.Hkv * (a.kv_mul / G) * a.max_splits;
-  if constexpr (wide_fits<T, D, G>()) {
-    if (a.wide && a.max_splits == 1) {
+  bool wide = false;
+  if constexpr (wide_fits<T, D, G>()) wide = a.wide != 0;
+  if (wide) {
+    if constexpr (wide_fits<T, D, G>()) {
       if (a.block_table)
         hipLaunchKernelGGL((decode_split_kernel<T, D, G, true, kWideWaves>), dim3((unsigned)blocks),
                            dim3(kWideWaves * kWave), 0, stream, a);
       else
         hipLaunchKernelGGL((decode_split_kernel<T, D, G, false, kWideWaves>),
                            dim3((unsigned)blocks), dim3(kWideWaves * kWave), 0, stream, a);
-      return hipGetLastError();
     }
-  }
-  if (a.block_table)
+  } else if (a.block_table) {
     hipLaunchKernelGGL((decode_split_kernel<T, D, G, true, kDecodeWaves>), dim3((unsigned)blocks),
                        dim3(kDecodeThreads), 0, stream, a);
-  else
+  } else {
     hipLaunchKernelGGL((decode_split_kernel<T, D, G, false, kDecodeWaves>), dim3((unsigned)blocks),
                        dim3(kDecodeThreads), 0, stream, a);
+  }
   if (a.max_splits > 1)
     hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.n_rows * a.Hq)), dim3(64),
                        0, stream, a);
