@@ -44,6 +44,23 @@
 
 #include <type_traits>
 
+#ifdef ORIN_PP_TIMELINE
+// Timeline build (orinmllm_amd/microbench/prefill_timeline.hip only; the library never
+// defines it): per workgroup, wave 0 stamps the 100 MHz wall clock at [0] entry, [1] first
+// K/V stage landed, [2] main-loop entry, and each wave w at [3 + w] the end of its tiles;
+// [11] = tiles, [12] = shader clocks of wave 0 from entry to [3].
+__device__ unsigned long long orin_pp_timeline[8192 * 16];
+#define PP_STAMP(i, cond)                                                         \
+  do {                                                                            \
+    if ((cond) && lane == 0 && blockIdx.x < 8192)                                 \
+      orin_pp_timeline[(long)blockIdx.x * 16 + (i)] = wall_clock64();             \
+  } while (0)
+#else
+#define PP_STAMP(i, cond) \
+  do {                    \
+  } while (0)
+#endif
+
 namespace orin {
 
 namespace {
@@ -173,8 +190,10 @@ __device__ __forceinline__ u32x2 lds_read_tr(lds_ptr p, int byte_off) {
 }
 
 // Key split of causal query block qb (rows qb*PBM ..): `diag` = the first tile holding a
-// key past the block's first query position; tiles [0, diag) are cut into chunks of C
-// tiles and tiles [diag, tiles) join the last chunk, so every chunk shows each of the
+// key past the block's first query position.  The block's tiles are cut into
+// ceil(tiles / C) chunks of near-equal length (C = the longest chunk the host allows),
+// at most diag + 1 of them, with every cut at or before diag: each chunk but the last is
+// unmasked, and the last holds tiles [diag, tiles), so every chunk shows each of the
 // block's queries at least one key.
 __host__ __device__ inline int pp_block_tiles(const FwdArgs& a, int qb) {
   return (a.start_pos + min((qb + 1) * PBM, a.n_q) + PBN - 1) / PBN;
@@ -184,7 +203,18 @@ __host__ __device__ inline int pp_block_diag(const FwdArgs& a, int qb) {
 }
 __host__ __device__ inline int pp_block_chunks(const FwdArgs& a, int qb, int C) {
   const int diag = pp_block_diag(a, qb);
-  return diag > 0 ? (diag + C - 1) / C : 1;
+  if (diag <= 0) return 1;
+  return min((pp_block_tiles(a, qb) + C - 1) / C, diag + 1);
+}
+// First tile of chunk c (0 <= c <= n, n = pp_block_chunks): the even cut c * tiles / n,
+// clamped to diag - (n - 1 - c) so that the cuts stay strictly increasing and the last one
+// is at most diag.  Both sequences rise by at least one per chunk (tiles >= n), so no
+// chunk is empty.
+__host__ __device__ inline int pp_chunk_lo(const FwdArgs& a, int qb, int n, int c) {
+  const int tiles = pp_block_tiles(a, qb);
+  if (c <= 0) return 0;
+  if (c >= n) return tiles;
+  return min((int)((long)c * tiles / n), pp_block_diag(a, qb) - (n - 1 - c));
 }
 // Work item `item` of a key-split launch, query blocks last to first: block qb, chunk c.
 __host__ __device__ inline void pp_item(const FwdArgs& a, int item, int C, int* qb, int* c) {
@@ -360,6 +390,10 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 #endif
   const int grp = PP_GRP == 0 ? (wave >> 2) : (wave & 1);
   const int lq = lane & 31, hf = lane >> 5;
+#ifdef ORIN_PP_TIMELINE
+  const unsigned long long tl_c0 = clock64();
+#endif
+  PP_STAMP(0, wave == 0);
 
   // ------------------------------------------------------------ block -> (head, rows)
   int head, q_lo, q_n, seg_start, kv_end, pos_off;
@@ -371,8 +405,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     int qb, c;
     pp_item(a, (int)blockIdx.x / a.Hq, C, &qb, &c);
     const int n_ch = pp_block_chunks(a, qb, C);
-    t_lo = c * C;
-    t_hi_split = c + 1 < n_ch ? (c + 1) * C : pp_block_tiles(a, qb);
+    t_lo = pp_chunk_lo(a, qb, n_ch, c);
+    t_hi_split = pp_chunk_lo(a, qb, n_ch, c + 1);
     partial = n_ch > 1;
     q_lo = qb * PBM;
     q_n = a.n_q;
@@ -516,6 +550,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
   wait_stage(min(n_tiles, PSTAGES - 1));
   step_barrier();
+  PP_STAMP(1, wave == 0);
 
   f32x16 oacc[DT];
 #pragma unroll
@@ -744,6 +779,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     ++k;
   };
   const int n_loop = n_tiles - 1;
+  PP_STAMP(2, wave == 0);
   for (int t = 0; t < n_loop; t += PSTAGES) {
     tile(t, std::integral_constant<int, 1>{});
     if (t + 1 < n_loop) tile(t + 1, std::integral_constant<int, 2>{});
@@ -773,6 +809,13 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 
   // ------------------------------------------------------------ normalise and store
+  PP_STAMP(3 + wave, true);
+#ifdef ORIN_PP_TIMELINE
+  if (lane == 0 && wave == 0 && blockIdx.x < 8192) {
+    orin_pp_timeline[(long)blockIdx.x * 16 + 11] = (unsigned long long)n_tiles;
+    orin_pp_timeline[(long)blockIdx.x * 16 + 12] = clock64() - tl_c0;
+  }
+#endif
   const float l_tot = l_run + partner32(l_run);
   const float inv = 1.f / l_tot;
   if (partial) {
@@ -952,14 +995,21 @@ int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
   if (!fwd_pp_supports(a, dtype) || a.n_q <= 0 || n_cu <= 0) return 0;
   const int nqb = (a.n_q + PBM - 1) / PBM;
   if ((long)nqb * a.Hq >= n_cu) return 0;  // the plain launch fills the device
-  // Smallest chunk that keeps the launch to one workgroup per CU; no split if that does
-  // not shorten the longest block by at least a third.
+  // Smallest chunk bound that keeps the launch to one workgroup per CU; no split if that
+  // does not shorten the longest block by at least a third.
   const int longest = pp_block_tiles(a, nqb - 1);
   for (int C = 1; C <= longest; ++C) {
     if ((long)pp_items(a, C) * a.Hq > n_cu) continue;
-    if (pp_block_chunks(a, nqb - 1, C) > kMergeMaxChunks) continue;
-    const int diag_extra = longest - pp_block_diag(a, nqb - 1);
-    if (3 * (C + diag_extra) > 2 * longest) return 0;
+    int worst = 0;  // longest chunk of the launch
+    bool fits = true;
+    for (int b = 0; b < nqb && fits; ++b) {
+      const int n = pp_block_chunks(a, b, C);
+      fits = n <= kMergeMaxChunks;
+      for (int c = 0; c < n; ++c)
+        worst = max(worst, pp_chunk_lo(a, b, n, c + 1) - pp_chunk_lo(a, b, n, c));
+    }
+    if (!fits) continue;
+    if (3 * worst > 2 * longest) return 0;
     const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
     const size_t part_bytes = dtype == kF16 ? 2 : 4;  // PartT
     *ws_bytes = rows * a.head_size * part_bytes + rows * 2 * sizeof(float);

@@ -55,10 +55,10 @@ struct FwdArgs {
   int n_seg, max_seqlen;
   int Hq, Hkv, kv_mul, head_size;
   float scale_log2;
-  // Causal key split (fwd_pp.hip): > 0 cuts each query block's keys before its diagonal
-  // into chunks of this many 64-key tiles (the diagonal tiles join the last chunk); the
-  // chunks of a block write fp32 partials to ws (unnormalised O rows, then (m, l)) and a
-  // second launch merges them.  0 = off.
+  // Causal key split (fwd_pp.hip): > 0 cuts each query block's 64-key tiles into
+  // near-equal chunks of at most this many tiles (the last chunk holds the diagonal
+  // tiles); the chunks of a block write partials to ws (O / l rows, then fp32 (m, l)) and
+  // a second launch merges them.  0 = off.
   int key_chunk_tiles;
   float* ws;
   // Fused Q producer (fwd_pp.hip, causal, head sizes 64 / 128): q holds the raw query rows;

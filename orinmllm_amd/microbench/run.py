@@ -15,9 +15,14 @@ import sys
 import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-PROGRAMS = ["hbm_stream", "coissue", "lds_read_rate", "lds_dma_issue", "lds_tr_layout"]
+PROGRAMS = ["hbm_stream", "coissue", "lds_read_rate", "lds_dma_issue", "lds_tr_layout",
+            "prefill_timeline"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+PKG = os.path.dirname(HERE)
+# prefill_timeline compiles the library's fwd_pp.hip into itself with the timeline stamps on.
+EXTRA = {"prefill_timeline": ["-I", os.path.join(PKG, "csrc"), "-I", os.path.join(os.path.dirname(PKG), "include"),
+                              "-DORIN_PP_TIMELINE"]}
 
 
 def main(argv: list[str]) -> int:
@@ -27,7 +32,7 @@ def main(argv: list[str]) -> int:
         for name in names:
             src = os.path.join(HERE, name + ".hip")
             exe = os.path.join(tmp, name)
-            res = subprocess.run([hipcc, *FLAGS, src, "-o", exe], capture_output=True, text=True)
+            res = subprocess.run([hipcc, *FLAGS, *EXTRA.get(name, []), src, "-o", exe], capture_output=True, text=True)
             if res.returncode != 0:
                 print(res.stderr, file=sys.stderr)
                 return 1
