@@ -1,4 +1,5 @@
-// Per-workgroup timeline of the ping-pong prefill (fwd_pp_kernel) on C2 and C3 fp16.
+// Per-workgroup timeline of the ping-pong prefill (fwd_pp_kernel) on C2, C3 and the C5
+// vision shape (bidirectional, d 64 / 72 / 128), fp16.
 //
 // fwd_pp.hip is compiled into this program with ORIN_PP_TIMELINE, which makes wave 0 of
 // every workgroup stamp the 100 MHz wall clock at entry, when its first K/V stage has
@@ -43,13 +44,18 @@ static void fill_normal(std::vector<orin::f16>& x, unsigned long long seed) {
   }
 }
 
-static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu) {
-  const size_t nq = (size_t)S * Hq * d, nkv = (size_t)S * Hkv * d;
+// causal: one sequence of S tokens; otherwise n_seg bidirectional segments of S tokens each
+// (the vision layout, cu_seqlens = 0, S, 2S, ...).
+static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu, int n_seg = 0) {
+  const bool causal = n_seg == 0;
+  const int n_tok = causal ? S : S * n_seg;
+  const size_t nq = (size_t)n_tok * Hq * d, nkv = (size_t)n_tok * Hkv * d;
   std::vector<orin::f16> hq(nq), hk(nkv), hv(nkv);
   fill_normal(hq, 1);
   fill_normal(hk, 2);
   fill_normal(hv, 3);
   void *q, *k, *v, *o, *ws = nullptr;
+  int* cu = nullptr;
   CHECK(hipMalloc(&q, nq * 2));
   CHECK(hipMalloc(&k, nkv * 2));
   CHECK(hipMalloc(&v, nkv * 2));
@@ -69,24 +75,33 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu)
   a.o = o;
   a.o_tok_stride = (long)Hq * d;
   a.o_head_stride = d;
-  a.n_q = S;
+  a.n_q = n_tok;
+  if (!causal) {
+    std::vector<int> hcu(n_seg + 1);
+    for (int i = 0; i <= n_seg; ++i) hcu[i] = i * S;
+    CHECK(hipMalloc(&cu, (n_seg + 1) * sizeof(int)));
+    CHECK(hipMemcpy(cu, hcu.data(), (n_seg + 1) * sizeof(int), hipMemcpyHostToDevice));
+    a.cu_seqlens = cu;
+    a.n_seg = n_seg;
+    a.max_seqlen = S;
+  }
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.kv_mul = Hq / Hkv;
   a.head_size = d;
   a.scale_log2 = (float)(1.0 / sqrt((double)d)) * orin::kLog2e;
   size_t ws_bytes = 0;
-  const int chunk = orin::fwd_pp_key_split(a, orin::kF16, n_cu, &ws_bytes);
+  const int chunk = causal ? orin::fwd_pp_key_split(a, orin::kF16, n_cu, &ws_bytes) : 0;
   if (chunk > 0) {
     CHECK(hipMalloc(&ws, ws_bytes));
     a.key_chunk_tiles = chunk;
     a.ws = (float*)ws;
   }
-  for (int i = 0; i < 20; ++i) CHECK(orin::launch_fwd_pp(a, orin::kF16, true, 0));
+  for (int i = 0; i < 20; ++i) CHECK(orin::launch_fwd_pp(a, orin::kF16, causal, 0));
   CHECK(hipDeviceSynchronize());
   std::vector<unsigned long long> zero(8192 * 16, 0), t(8192 * 16);
   CHECK(hipMemcpyToSymbol(HIP_SYMBOL(orin_pp_timeline), zero.data(), zero.size() * 8));
-  CHECK(orin::launch_fwd_pp(a, orin::kF16, true, 0));
+  CHECK(orin::launch_fwd_pp(a, orin::kF16, causal, 0));
   CHECK(hipDeviceSynchronize());
   CHECK(hipMemcpyFromSymbol(t.data(), HIP_SYMBOL(orin_pp_timeline), t.size() * 8));
 
@@ -117,8 +132,9 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu)
     sxy += tiles * dur;
   }
   const double slope = (n * sxy - sx * sy) / (n * sxx - sx * sx), icpt = (sy - slope * sx) / n;
-  printf("%s: S %d, %d/%d heads, d %d, key split %s (chunk bound %d tiles): %d workgroups, span %.2f us\n",
-         name, S, Hq, Hkv, d, chunk > 0 ? "on" : "off", chunk, n, (t_end - t0) / 100.0);
+  printf("%s: %s %d x %d tokens, %d/%d heads, d %d, key split %s (chunk bound %d tiles): %d workgroups, span %.2f us\n",
+         name, causal ? "causal" : "bidirectional", causal ? 1 : n_seg, S, Hq, Hkv, d,
+         chunk > 0 ? "on" : "off", chunk, n, (t_end - t0) / 100.0);
   printf("| tiles | workgroups | duration us | first stage landed us | loop entry us | shader GHz |\n");
   printf("|---|---|---|---|---|---|\n");
   for (auto& kv : by_tiles) {
@@ -132,6 +148,7 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu)
   CHECK(hipFree(v));
   CHECK(hipFree(o));
   if (ws) CHECK(hipFree(ws));
+  if (cu) CHECK(hipFree(cu));
 }
 
 int main() {
@@ -140,5 +157,8 @@ int main() {
   CHECK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
   run_shape("C2", 2048, 12, 2, 128, n_cu);
   run_shape("C3", 4096, 32, 8, 128, n_cu);
+  run_shape("C5 (fp16)", 1024, 16, 16, 72, n_cu, 4);
+  run_shape("C5 shape at d 64", 1024, 16, 16, 64, n_cu, 4);
+  run_shape("C5 shape at d 128", 1024, 16, 16, 128, n_cu, 4);
   return 0;
 }
