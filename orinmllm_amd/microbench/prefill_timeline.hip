@@ -142,7 +142,8 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu,
     printf("| %d | %d | %.2f | %.2f | %.2f | %.2f |\n", kv.first, c.n, c.dur / c.n, c.first / c.n,
            c.loop / c.n, c.ghz / c.n);
   }
-  printf("fit: duration = %.3f us/tile + %.3f us\n\n", slope, icpt);
+  if (by_tiles.size() > 1) printf("fit: duration = %.3f us/tile + %.3f us\n", slope, icpt);
+  printf("\n");
   CHECK(hipFree(q));
   CHECK(hipFree(k));
   CHECK(hipFree(v));
