@@ -55,9 +55,24 @@ __device__ unsigned long long orin_pp_timeline[8192 * 16];
     if ((cond) && lane == 0 && blockIdx.x < 8192)                                 \
       orin_pp_timeline[(long)blockIdx.x * 16 + (i)] = wall_clock64();             \
   } while (0)
+// Steps kStepStamp0 .. +3 of waves 0 (group 0) and 4 (group 1), which share a SIMD: shader
+// clock at [0] the step's start, [1] the end of the wave's phase work (its last MFMA or
+// softmax instruction issued), [2] the step's exit from the barrier.
+constexpr int kStepStamp0 = 12;
+__device__ unsigned long long orin_pp_steps[8192 * 2 * 4 * 3];
+#define PP_STEP_STAMP(k, j)                                                                \
+  do {                                                                                     \
+    if (lane == 0 && (wave & 3) == 0 && (k) >= kStepStamp0 && (k) < kStepStamp0 + 4 &&    \
+        blockIdx.x < 8192)                                                                 \
+      orin_pp_steps[(((long)blockIdx.x * 2 + (wave >> 2)) * 4 + (k) - kStepStamp0) * 3 + (j)] = \
+          clock64();                                                                       \
+  } while (0)
 #else
 #define PP_STAMP(i, cond) \
   do {                    \
+  } while (0)
+#define PP_STEP_STAMP(k, j) \
+  do {                      \
   } while (0)
 #endif
 
@@ -767,16 +782,22 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // the QK product of the next tile, also for a wave whose queries all precede it: one
   // MFMA-phase shape inside the loop keeps the accumulators in fixed registers.
   auto tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
+    PP_STEP_STAMP(k, 0);
     step_begin(k);
     __builtin_amdgcn_s_setprio(1);
     if (active(t)) mphase(slot_tag, std::true_type{});
     __builtin_amdgcn_s_setprio(0);
+    PP_STEP_STAMP(k, 1);
     step_end(k);
     ++k;
+    PP_STEP_STAMP(k - 1, 2);
+    PP_STEP_STAMP(k, 0);
     step_begin(k);
     if (active(t + 1)) softmax(t + 1);
+    PP_STEP_STAMP(k, 1);
     step_end(k);
     ++k;
+    PP_STEP_STAMP(k - 1, 2);
   };
   const int n_loop = n_tiles - 1;
   PP_STAMP(2, wave == 0);

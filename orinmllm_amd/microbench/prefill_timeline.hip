@@ -8,7 +8,9 @@
 // recorded launch.  Printed per distinct tile count: workgroups, mean duration, the three
 // prologue stamps, and a least-squares fit duration = a * tiles + b (b = the fixed cost a
 // workgroup pays whatever its work: argument fetch, Q load, the first stages' latency, the
-// pipeline's fill and drain steps).
+// pipeline's fill and drain steps).  Then, for steps 12-15 of waves 0 and 4 (one of each
+// ping-pong group, on one SIMD), the shader clocks of the wave's own phase work and of the
+// whole step up to its barrier, split by the phase the wave ran (MFMA or softmax).
 //
 // Build and run: python orinmllm_amd/microbench/run.py prefill_timeline
 #include "fwd_pp.hip"
@@ -99,8 +101,9 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu,
   }
   for (int i = 0; i < 20; ++i) CHECK(orin::launch_fwd_pp(a, orin::kF16, causal, 0));
   CHECK(hipDeviceSynchronize());
-  std::vector<unsigned long long> zero(8192 * 16, 0), t(8192 * 16);
-  CHECK(hipMemcpyToSymbol(HIP_SYMBOL(orin_pp_timeline), zero.data(), zero.size() * 8));
+  std::vector<unsigned long long> zero(8192 * 24, 0), t(8192 * 16);
+  CHECK(hipMemcpyToSymbol(HIP_SYMBOL(orin_pp_timeline), zero.data(), t.size() * 8));
+  CHECK(hipMemcpyToSymbol(HIP_SYMBOL(orin_pp_steps), zero.data(), zero.size() * 8));
   CHECK(orin::launch_fwd_pp(a, orin::kF16, causal, 0));
   CHECK(hipDeviceSynchronize());
   CHECK(hipMemcpyFromSymbol(t.data(), HIP_SYMBOL(orin_pp_timeline), t.size() * 8));
@@ -143,6 +146,27 @@ static void run_shape(const char* name, int S, int Hq, int Hkv, int d, int n_cu,
            c.loop / c.n, c.ghz / c.n);
   }
   if (by_tiles.size() > 1) printf("fit: duration = %.3f us/tile + %.3f us\n", slope, icpt);
+  // Steady-state steps: per group, the mean of (phase work, step) over the workgroups that
+  // reached them; group 0 runs its MFMA phase in even steps, group 1 in odd ones.
+  std::vector<unsigned long long> st(8192 * 24);
+  CHECK(hipMemcpyFromSymbol(st.data(), HIP_SYMBOL(orin_pp_steps), st.size() * 8));
+  double work[2][2] = {{0, 0}, {0, 0}}, step[2][2] = {{0, 0}, {0, 0}};
+  int cnt[2][2] = {{0, 0}, {0, 0}};
+  for (int b = 0; b < n; ++b)
+    for (int g = 0; g < 2; ++g)
+      for (int q = 0; q < 4; ++q) {
+        const unsigned long long* e = &st[((b * 2 + g) * 4 + q) * 3];
+        if (!e[0] || !e[1] || !e[2]) continue;
+        const int mf = ((kStepStamp0 + q) & 1) == g ? 1 : 0;  // group g's MFMA phase?
+        work[g][mf] += (double)(e[1] - e[0]);
+        step[g][mf] += (double)(e[2] - e[0]);
+        cnt[g][mf]++;
+      }
+  for (int g = 0; g < 2; ++g)
+    for (int mf = 1; mf >= 0; --mf)
+      if (cnt[g][mf])
+        printf("group %d %s step: work %.0f clocks, step %.0f clocks (%d samples)\n", g,
+               mf ? "MFMA   " : "softmax", work[g][mf] / cnt[g][mf], step[g][mf] / cnt[g][mf], cnt[g][mf]);
   printf("\n");
   CHECK(hipFree(q));
   CHECK(hipFree(k));

@@ -16,7 +16,7 @@ import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PROGRAMS = ["hbm_stream", "coissue", "lds_read_rate", "lds_dma_issue", "lds_tr_layout",
-            "prefill_timeline"]
+            "prefill_timeline", "pingpong_coissue"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 PKG = os.path.dirname(HERE)
