@@ -1019,27 +1019,31 @@ int fwd_pp_key_split(const FwdArgs& a, int dtype, int n_cu, size_t* ws_bytes) {
   if (!fwd_pp_supports(a, dtype) || a.n_q <= 0 || n_cu <= 0) return 0;
   const int nqb = (a.n_q + PBM - 1) / PBM;
   if ((long)nqb * a.Hq >= n_cu) return 0;  // the plain launch fills the device
-  // Smallest chunk bound that keeps the launch to one workgroup per CU; no split if that
-  // does not shorten the longest block by at least a third.
+  // Smallest chunk bound that keeps the launch to one workgroup per CU and each block to
+  // at most kMergeMaxChunks chunks (both counts fall as C grows: binary search); no split
+  // if that does not shorten the longest block by at least a third.
   const int longest = pp_block_tiles(a, nqb - 1);
-  for (int C = 1; C <= longest; ++C) {
-    if ((long)pp_items(a, C) * a.Hq > n_cu) continue;
-    int worst = 0;  // longest chunk of the launch
-    bool fits = true;
-    for (int b = 0; b < nqb && fits; ++b) {
-      const int n = pp_block_chunks(a, b, C);
-      fits = n <= kMergeMaxChunks;
-      for (int c = 0; c < n; ++c)
-        worst = max(worst, pp_chunk_lo(a, b, n, c + 1) - pp_chunk_lo(a, b, n, c));
-    }
-    if (!fits) continue;
-    if (3 * worst > 2 * longest) return 0;
-    const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
-    const size_t part_bytes = dtype == kF16 ? 2 : 4;  // PartT
-    *ws_bytes = rows * a.head_size * part_bytes + rows * 2 * sizeof(float);
-    return C;
+  auto fits = [&](int C) {
+    return (long)pp_items(a, C) * a.Hq <= n_cu && pp_block_chunks(a, nqb - 1, C) <= kMergeMaxChunks;
+  };
+  if (!fits(longest)) return 0;
+  int lo = 1, hi = longest;
+  while (lo < hi) {
+    const int mid = lo + (hi - lo) / 2;
+    if (fits(mid)) hi = mid; else lo = mid + 1;
   }
-  return 0;
+  const int C = lo;
+  int worst = 0;  // longest chunk of the launch
+  for (int b = 0; b < nqb; ++b) {
+    const int n = pp_block_chunks(a, b, C);
+    for (int c = 0; c < n; ++c)
+      worst = max(worst, pp_chunk_lo(a, b, n, c + 1) - pp_chunk_lo(a, b, n, c));
+  }
+  if (3 * worst > 2 * longest) return 0;
+  const size_t rows = (size_t)pp_items(a, C) * a.Hq * PBM;
+  const size_t part_bytes = dtype == kF16 ? 2 : 4;  // PartT
+  *ws_bytes = rows * a.head_size * part_bytes + rows * 2 * sizeof(float);
+  return C;
 }
 
 hipError_t launch_fwd_pp(const FwdArgs& a, int dtype, bool causal, hipStream_t stream) {
