@@ -266,10 +266,12 @@ decode_split_kernel(DecodeArgs a) {
   const float c = a.scale_log2;
   // Per-lane offsets (elements) inside an 8-token step, used when the whole tile lies
   // below s1: K token group grp, V token r.
-  const int k_off = grp * (int)map.tok_stride + k_lane;
-  int v_off[8];
+  // Offsets are unsigned 32-bit byte offsets from a wave-uniform row base, so the loads use
+  // the SGPR-base + VGPR-offset addressing form instead of 64-bit per-lane addresses.
+  const uint32_t k_off = (uint32_t)(grp * (int)map.tok_stride + k_lane) * sizeof(T);
+  uint32_t v_off[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) v_off[r] = r * (int)map.tok_stride + v_lane;
+  for (int r = 0; r < 8; ++r) v_off[r] = (uint32_t)(r * (int)map.tok_stride + v_lane) * sizeof(T);
 
   // Block ids of the K steps / V tokens of the tile at t0.  In a tile that crosses s1,
   // tokens >= s1 read row s1-1 (finite data; their weights are 0).
@@ -282,12 +284,14 @@ decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       const int step_tok = min(t0 + s * 8, s1 - 1);  // uniform
-      const T* rowp = kb + map.row_offset(step_tok, blk[s]);
-      const int lo = full ? k_off
-                          : (min(t0 + s * 8 + grp, s1 - 1) - step_tok) * (int)map.tok_stride +
-                                k_lane;
+      const char* rowp = reinterpret_cast<const char*>(kb + map.row_offset(step_tok, blk[s]));
+      const uint32_t lo =
+          full ? k_off
+               : (uint32_t)((min(t0 + s * 8 + grp, s1 - 1) - step_tok) * (int)map.tok_stride +
+                            k_lane) * sizeof(T);
 #pragma unroll
-      for (int n = 0; n < NV; ++n) dst[s][n] = load_chunk_nt(rowp + lo + n * S::CH_STRIDE);
+      for (int n = 0; n < NV; ++n)
+        dst[s][n] = load_chunk_nt(reinterpret_cast<const T*>(rowp + lo + n * S::CH_STRIDE * sizeof(T)));
     }
   };
   // V token j = 8s + r of the tile lies in the block of K step s; the step's row address
@@ -297,12 +301,13 @@ decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       const int step_tok = min(t0 + s * 8, s1 - 1);
-      const T* rowp = vb + map.row_offset(step_tok, blk[s]);
+      const char* rowp = reinterpret_cast<const char*>(vb + map.row_offset(step_tok, blk[s]));
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        const int off = full ? v_off[r]
-                             : (min(t0 + s * 8 + r, s1 - 1) - step_tok) * (int)map.tok_stride +
-                                   v_lane;
+        const uint32_t off =
+            full ? v_off[r]
+                 : (uint32_t)((min(t0 + s * 8 + r, s1 - 1) - step_tok) * (int)map.tok_stride +
+                              v_lane) * sizeof(T);
         dst[s * 8 + r] = __builtin_nontemporal_load(reinterpret_cast<const VR*>(rowp + off));
       }
     }
