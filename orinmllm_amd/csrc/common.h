@@ -130,12 +130,38 @@ __device__ __forceinline__ float chunk_dot(const Chunk<bf16>& a, const Chunk<bf1
                                           false);
   return acc;
 }
+// chunk_dot with a zero accumulator.  For 16-bit chunks the first product is the
+// three-operand v_dot2 with an inline 0 (the compiler otherwise zeroes a register with a
+// v_mov and accumulates into it with v_dot2c).
+__device__ __forceinline__ float chunk_dot_first(const Chunk<f16>& a, const Chunk<f16>& b) {
+  const f16x8 x = __builtin_bit_cast(f16x8, a.raw), y = __builtin_bit_cast(f16x8, b.raw);
+  float acc;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(acc) : "v"(f16x2{x[0], x[1]}), "v"(f16x2{y[0], y[1]}));
+#pragma unroll
+  for (int i = 1; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2(f16x2{x[2 * i], x[2 * i + 1]},
+                                 f16x2{y[2 * i], y[2 * i + 1]}, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float chunk_dot_first(const Chunk<bf16>& a, const Chunk<bf16>& b) {
+  const bf16x8 x = __builtin_bit_cast(bf16x8, a.raw), y = __builtin_bit_cast(bf16x8, b.raw);
+  float acc;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(bf16x2{x[0], x[1]}), "v"(bf16x2{y[0], y[1]}));
+#pragma unroll
+  for (int i = 1; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{x[2 * i], x[2 * i + 1]},
+                                          bf16x2{y[2 * i], y[2 * i + 1]}, acc, false);
+  return acc;
+}
 __device__ __forceinline__ float chunk_dot(const Chunk<float>& a, const Chunk<float>& b,
                                            float acc) {
   const f32x4 x = __builtin_bit_cast(f32x4, a.raw), y = __builtin_bit_cast(f32x4, b.raw);
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(x[i], y[i], acc);
   return acc;
+}
+__device__ __forceinline__ float chunk_dot_first(const Chunk<float>& a, const Chunk<float>& b) {
+  return chunk_dot(a, b, 0.f);
 }
 
 // Unpack a chunk into fp32 values.
@@ -181,10 +207,13 @@ constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8-lane half row
 constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i+8) mod 16 inside a row
 
+// No "old" operand (bound_ctrl set): the controls used here give every lane a valid
+// source, and the compiler can fold the move into the consuming v_add / v_max as a DPP
+// operand instead of zeroing a register first.
 template <int kCtrl>
 __device__ __forceinline__ float dpp_mov(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, true));
 }
 
 // Sum over each aligned group of 8 lanes; every lane of the group gets the sum.

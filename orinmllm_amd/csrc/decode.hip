@@ -332,9 +332,9 @@ decode_split_kernel(DecodeArgs a) {
         const bool valid = t0 + s * 8 + grp < s1;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          float d = 0.f;
+          float d = chunk_dot_first(qc[g][0], kc[s][0]);
 #pragma unroll
-          for (int n = 0; n < NV; ++n) d = chunk_dot(qc[g][n], kc[s][n], d);
+          for (int n = 1; n < NV; ++n) d = chunk_dot(qc[g][n], kc[s][n], d);
           d = sum8(d);
           sc[s][g] = valid ? d * c : -INFINITY;
         }
