@@ -493,9 +493,10 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   char* const v_lds = smem + PKREGION;
   const uint32_t k_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
 
-  // Stage u = K(u) + V(u-1) into ring slot u % 3.  Rows past the sequence (and V(-1))
-  // read a valid row instead, so every stage is exactly four transfers per wave and
-  // LDS never holds non-finite garbage.
+  // Stage u = K(u) + V(u-1) into ring slot u % 3 (stage 0: K(0) only).  Rows past the
+  // sequence read a valid row instead, so every stage after the first is exactly four
+  // transfers per wave (the waits count them from the youngest stage) and the LDS rows the
+  // MFMA phases read never hold non-finite garbage.
   // Addresses: a wave-uniform tile base (scalar) plus a per-lane byte offset
   // row_in_tile * row_bytes + column bytes (`fwd_pp_supports` keeps row_bytes below 2^24,
   // so one 24-bit multiply-add forms it).
@@ -518,6 +519,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       const int rv = k_row[i] < v_last ? k_row[i] : v_last;
       dma16_s(kt_base, __umul24(rk, row_bytes) + k_col[i] * (uint32_t)sizeof(T),
               k_base + sl * PTILE_BYTES + b * 1024);
+      if (u == 0) continue;  // V(-1): no MFMA phase reads it
       dma16_s(vt_base, __umul24(rv, row_bytes) + v_col[i] * (uint32_t)sizeof(T),
               k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
     }
