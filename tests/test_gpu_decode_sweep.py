@@ -77,3 +77,32 @@ def test_paged_decode_sweep(i, kind, B, Hq, Hkv, d, bs, layout, split):
         assert_fp32_close(got1[live], ref, d, what=f"sweep case {i} whole-row")
     else:
         assert_lowp_close(got1[live], ref, what=f"sweep case {i} whole-row")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("B,Hq,Hkv,d", [(1, 32, 8, 128), (2, 12, 2, 128), (3, 16, 4, 64)])
+@pytest.mark.parametrize("split", [64, 256])
+def test_small_launch_split_decode(kind, B, Hq, Hkv, d, split):
+    """Launches with no more workgroups than CUs (here at most 3 rows x 8 kv heads x 32
+    splits) run 16-wave workgroups per split where the shape allows, then the merge; the
+    result must match the oracle and be bit-equal between paged and contiguous caches."""
+    rng = np.random.default_rng(4100 + B * 10 + d + split)
+    lens = np.array([2048, 300, 1][:B], np.int32)
+    kc, vc, kp, vp, bt = make_paged(rng, lens, Hkv, d, 16, kind)
+    q = quantize(normal(rng, (B, Hq, d)), kind)
+    lens_d = torch.from_numpy(lens).cuda()
+    maxlen = int(lens.max())
+    op = torch.full((B, Hq, d), 7.0, device="cuda", dtype=TORCH[kind])
+    oc = torch.zeros_like(op)
+    K.paged_decode_cu(dev(q, kind), dev(kp, kind), dev(vp, kind), op, torch.from_numpy(bt).cuda(),
+                      lens_d, maxlen, split_tokens=split, layout=K.KV_LAYOUT_TOKEN_MAJOR)
+    K.batched_decode_cu(dev(q, kind), dev(kc, kind), dev(vc, kind), oc, lens_d, maxlen, Hkv,
+                        split_tokens=split)
+    torch.cuda.synchronize()
+    assert torch.equal(op, oc), "small launch: paged != contiguous"
+    ref = oracle.decode_contig(q, kc, vc, lens)
+    if kind == "fp32":
+        assert_fp32_close(host(op), ref, d, what=f"small launch {kind} B{B} split {split}")
+    else:
+        assert_lowp_close(host(op), ref, what=f"small launch {kind} B{B} split {split}")
