@@ -73,11 +73,13 @@ def test_pp_causal_small_head(kind, d):
 @pytest.mark.parametrize("start_pos,S,Hq,Hkv,d", [(0, 2048, 12, 2, 128), (100, 2049, 12, 2, 128),
                                                   (0, 1024, 32, 8, 128), (0, 300, 12, 2, 128),
                                                   (37, 600, 4, 1, 128), (0, 1500, 12, 12, 128),
-                                                  (5, 1800, 8, 2, 64), (0, 2048, 6, 3, 96)])
+                                                  (5, 1800, 8, 2, 64), (0, 2048, 6, 3, 96),
+                                                  (6000, 520, 8, 2, 128), (3000, 257, 4, 1, 64)])
 def test_pp_causal_key_split(kind, start_pos, S, Hq, Hkv, d):
-    """Causal launches with fewer 256-query blocks than CUs split each block's keys before
-    its diagonal into chunks (fp32 partials merged by a second launch)
-    (S 2048, 12 q / 2 kv heads) and ragged / prefixed / tiny variants."""
+    """Causal launches with fewer 256-query blocks than CUs cut each block's key tiles into
+    near-equal chunks (partials merged by a second launch): BASELINE config 2 (S 2048, 12 q /
+    2 kv heads), ragged / prefixed / tiny variants, and long prefixes (6000 and 3000 cached
+    tokens before a few hundred queries: up to 8 chunks per block, a one-row last block)."""
     rng = np.random.default_rng(start_pos + S + Hq)
     q, kc, vc, out = run_prefill(kind, start_pos, S, Hq, Hkv, d, start_pos + S, 1, 0, rng)
     rows = sample_rows(S, 60, rng)
