@@ -423,7 +423,7 @@ def main():
             traffic = json.load(f)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(every box has one MI355X; see DESIGN.md for how the path shards)",
+              "(every box has one MI355X; the multi-GPU path is a design, not a build)",
               file=sys.stderr)
         return 2
     import torch
