@@ -1,5 +1,5 @@
-"""The kuiper-side adapter given in the integration guide at the repository root (the kernel:: function bodies that
-forward to the C ABI) compiles and links: its C++ blocks are extracted, the kuiper
+"""The kuiper-side adapter given in the integration guide at the repository root (the
+kernel:: function bodies that forward to the C ABI) compiles and links: its C++ blocks are extracted, the kuiper
 include lines are replaced by tests/cpp/kuiper_names.h (kuiper's type names bound to
 the host mirror), and the result is built as a shared object with --no-undefined
 against liborin_attn.so, so every orin_* call it makes resolves with the declared
