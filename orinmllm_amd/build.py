@@ -18,7 +18,7 @@ REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "liborin_attn.so")
-SOURCES = ["decode.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "outproj.hip", "capi.hip"]
+SOURCES = ["decode.hip", "decode_mfma.hip", "fwd.hip", "fwd_pp.hip", "producers.hip", "outproj.hip", "capi.hip"]
 # C++ host mirror of kuiper's kernel:: functions and op:: layers over the C ABI.
 HOST_DIR = os.path.join(PKG_DIR, "cpp")
 HOST_SOURCES = ["base.cpp", "kernels.cpp", "layers.cpp"]

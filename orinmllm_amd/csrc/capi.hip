@@ -34,12 +34,21 @@ int round_up(long x, int m) { return (int)((x + m - 1) / m * m); }
 // The combine kernel merges at most this many splits per row.
 constexpr int kMaxSplits = 1024;
 
+int device_cus();
+
 // Tokens per split for a decode launch with `base_blocks` (row, kv head, head group)
-// units and rows of up to max_len tokens.  Aims at ~3328 workgroups (13 per CU, i.e.
-// about 3.25 rounds of the 4 resident per CU; measured best on the batch-32 paged
-// decode) with at least 256 tokens (one 64-token tile per wave) per split.
+// units and rows of up to max_len tokens.
+//  * At least one unit per CU: whole rows (one split), so no partials and no merge launch.
+//    Each unit is then one workgroup that streams its row (for 16-bit caches at head size
+//    64 / 128 on the matrix-core kernel).  Batch 32 x 8 kv heads (fp16, d 128): every
+//    length 4096 0.76-0.77 of HBM against 0.66 with 320-token splits; lengths U[512, 4096]
+//    0.64 against 0.62-0.63 with 320-token splits plus their merge.
+//  * Fewer units: aims at ~3328 workgroups (13 per CU, i.e. about 3.25 rounds of the 4
+//    resident per CU; measured best on the batch-32 paged decode) with at least 256 tokens
+//    (one 64-token tile per wave) per split.
 int auto_split_tokens(long base_blocks, int max_len) {
   if (max_len <= 0) return 256;
+  if (base_blocks >= device_cus()) return round_up(max_len, 64);
   const long target = 3328;
   long splits = (target + base_blocks - 1) / base_blocks;
   if (splits < 1) splits = 1;
@@ -148,14 +157,6 @@ int device_cus() {
   return cached;
 }
 
-bool wide_small_launches() {
-  static const bool on = [] {
-    const char* e = getenv("ORIN_DECODE_WIDE_SMALL");
-    return !(e && !strcmp(e, "0"));
-  }();
-  return on;
-}
-
 DecodeArgs decode_defaults() {
   DecodeArgs a = {};
   a.max_splits = 1;
@@ -180,11 +181,15 @@ int kuiper_decode_split(int head_num, int kv_head_num, int head_size, int max_le
 int run_decode(DecodeArgs& a, int dtype, int max_len, hipStream_t stream) {
   a.max_splits = n_splits(max_len, a.split_tokens);
   if (a.max_splits <= 1) a.max_splits = 1;
-  // 16-wave workgroups (where the shape fits) when each (row, kv head, head group) is one
-  // split, or when the launch has no more workgroups than the device has CUs: 4-wave
-  // workgroups would then leave most wave slots idle.
+  // Dot-product kernel: 16-wave workgroups (where the shape fits) when each (row, kv head,
+  // head group) is one split, or when the launch has no more workgroups than the device has
+  // CUs: 4-wave workgroups would then leave most wave slots idle.
   const long units = (long)a.n_rows * a.Hkv * (a.kv_mul / decode_heads_per_block(a.kv_mul));
-  a.wide = a.max_splits == 1 || (wide_small_launches() && units * a.max_splits <= device_cus());
+  a.wide = a.max_splits == 1 || units * a.max_splits <= device_cus();
+  // Whole rows of a launch with a (row, kv head) per CU or more: matrix-core kernel.  The
+  // single-sequence (kuiper) decode never qualifies, so its result does not depend on
+  // whether the launch was sized for the position or for the cache capacity.
+  a.mfma = a.max_splits == 1 && (long)a.n_rows * a.Hkv >= device_cus();
   a.len_cap = max_len > 0 ? max_len : (1 << 30);
   return hip_status(launch_decode(a, dtype, stream));
 }

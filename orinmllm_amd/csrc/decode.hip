@@ -31,6 +31,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "decode_rows.h"
 
 namespace orin {
 
@@ -153,31 +154,6 @@ struct TokenMap {
     return (long)tok * tok_stride;
   }
 };
-
-__device__ __forceinline__ int find_segment(const int* cu, int n_seg, int row) {
-  int lo = 0, hi = n_seg - 1;  // s with cu[s] <= row < cu[s+1]
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (cu[mid] <= row) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
-__device__ __forceinline__ int row_len_raw(const DecodeArgs& a, int row) {
-  if (a.cu_seqlens) {
-    const int s = find_segment(a.cu_seqlens, a.n_seg, row);
-    return a.cu_seqlens[s + 1] - a.cu_seqlens[s];
-  }
-  if (a.lens) return a.lens[row] + a.len_add;
-  return a.len_base + row * a.len_step;
-}
-
-// A device-side length (gpu pos, context_lens) longer than the launch was sized for
-// (len_cap, from the host's max_context_len / max_seq_len) is an argument error that the
-// host cannot see.  Such a row is not attended over a truncated prefix: its output is NaN.
-__device__ __forceinline__ int row_len(const DecodeArgs& a, int row) {
-  return row_len_raw(a, row);
-}
 
 template <typename T, int D, int G, bool PAGED, int NW>
 __global__ void __launch_bounds__(NW * kWave)
@@ -545,6 +521,14 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   for (int e = 0; e < EPL; ++e) out[threadIdx.x * EPL + e] = from_f32<T>(o[e] * inv);
 }
 
+template <typename T, int D>
+hipError_t launch_combine(const DecodeArgs& a, hipStream_t stream) {
+  if (a.max_splits > 1)
+    hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.n_rows * a.Hq)), dim3(64),
+                       0, stream, a);
+  return hipGetLastError();
+}
+
 template <typename T, int D, int G>
 hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_rows * a.Hkv * (a.kv_mul / G) * a.max_splits;
@@ -566,10 +550,7 @@ hipError_t launch_decode_tg(const DecodeArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((decode_split_kernel<T, D, G, false, kDecodeWaves>), dim3((unsigned)blocks),
                        dim3(kDecodeThreads), 0, stream, a);
   }
-  if (a.max_splits > 1)
-    hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3((unsigned)(a.n_rows * a.Hq)), dim3(64),
-                       0, stream, a);
-  return hipGetLastError();
+  return launch_combine<T, D>(a, stream);
 }
 
 template <typename T, int D>
@@ -611,6 +592,11 @@ bool decode_supports(int dtype, int head_size) {
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t stream) {
+  // Launches of whole rows that fill the device go to the matrix-core kernel, which streams
+  // a row faster per CU; split launches stay on the dot-product kernel, whose small
+  // workgroups balance ragged rows better.
+  if (a.mfma && a.max_splits == 1 && decode_mfma_supports(dtype, a.head_size, a.kv_mul))
+    return launch_decode_mfma(a, dtype, stream);
   const int G = decode_heads_per_block(a.kv_mul);
   switch (dtype) {
     case kF32: return launch_decode_d<float>(a, G, stream);

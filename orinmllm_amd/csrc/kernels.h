@@ -30,7 +30,9 @@ struct DecodeArgs {
   long o_row_stride, o_head_stride;
   float* ws;  // [n_rows, Hq, max_splits, head_size + 2] fp32 partials (unused if max_splits == 1)
   int max_splits, split_tokens;
-  int wide;  // one split per row: 16-wave workgroups where the shape fits (decode.hip)
+  int wide;  // dot-product kernel: 16-wave workgroups where the shape fits (decode.hip)
+  int mfma;  // one split per row and a unit per CU or more: the matrix-core kernel where it
+             // supports the shape (decode_mfma.hip)
   int n_rows, Hq, Hkv, kv_mul, head_size;
   float scale_log2;  // softmax scale * log2(e)
 };
@@ -38,6 +40,12 @@ struct DecodeArgs {
 int decode_heads_per_block(int kv_mul);
 bool decode_supports(int dtype, int head_size);
 hipError_t launch_decode(const DecodeArgs& a, int dtype, hipStream_t stream);
+// Matrix-core decode (decode_mfma.hip) for 16-bit caches, head sizes 64 / 128 and up to 16
+// query heads per kv head: one workgroup per (row, kv head, split) serving all kv_mul heads.
+// launch_decode routes the shapes it supports there.
+bool decode_mfma_supports(int dtype, int head_size, int kv_mul);
+size_t decode_mfma_lds_bytes(int head_size);
+hipError_t launch_decode_mfma(const DecodeArgs& a, int dtype, hipStream_t stream);
 
 // Tile-parallel attention forward on MFMA (fp16 / bf16): causal prefill over a
 // kuiper-layout cache, or bidirectional varlen segments.

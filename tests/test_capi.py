@@ -134,13 +134,17 @@ def test_missing_library_fails_loudly(tmp_path):
 
 
 def test_split_tokens_for_total():
-    """Near-uniform batches get one round of long splits; ragged ones the automatic size;
+    """A batch with a (row, kv head) per CU or more gets whole rows whatever its lengths;
+    smaller near-uniform batches one round of long splits, ragged ones the automatic size;
     bad arguments 0.  Host-only (the CU count query falls back to 256 without a GPU)."""
     lib = _lib.load()
     f = lib.orin_attn_decode_split_tokens_for_total
     auto = lib.orin_attn_decode_split_tokens(32, 32, 8, 4096, 0)
-    ragged = f(32, 32, 8, 4096, 74949)
-    uniform = f(32, 32, 8, 4096, 32 * 4096)
-    assert ragged == auto
-    assert uniform % 64 == 0 and uniform > auto
+    assert auto == 4096  # 32 x 8 = 256 units: whole rows
+    assert f(32, 32, 8, 4096, 74949) == auto and f(32, 32, 8, 4096, 32 * 4096) == auto
+    auto8 = lib.orin_attn_decode_split_tokens(8, 32, 8, 4096, 0)
+    ragged = f(8, 32, 8, 4096, 8 * 2000)
+    uniform = f(8, 32, 8, 4096, 8 * 4096)
+    assert auto8 < 4096 and ragged == auto8
+    assert uniform % 64 == 0 and uniform >= auto8
     assert f(0, 32, 8, 4096, 1) == 0 and f(32, 32, 7, 4096, 1) == 0 and f(32, 32, 8, 4096, -1) == 0
