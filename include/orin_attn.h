@@ -101,6 +101,12 @@ int orin_batched_mha(int32_t start_pos, int32_t seq_len, int32_t head_num, int32
  * reference's fp32 or fp16 variant; bf16 is new.  fp16/bf16 run on MFMA.  A 16-bit launch
  * with fewer 256-query blocks than the device has CUs splits the keys of each block and
  * keeps the partials in the stream's library-owned workspace (see below).
+ * bf16 range: the softmax weights and the weighted sum with V run in fp16 (V is converted
+ * to fp16 on chip), so bf16 V must satisfy |v| <= 65504; a larger value turns non-finite
+ * the outputs of every row that attends to it (and possibly of other rows whose 64-key
+ * tile holds it).  V elements below 2^-14 in magnitude keep
+ * fp16's subnormal spacing (absolute error at most 2^-25 each, hence in the output).  The
+ * decode entry points use bf16 V as stored and have neither limit.
  */
 int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t head_num,
                                  int32_t kv_head_num, int32_t head_size, int32_t kv_mul,
@@ -121,7 +127,7 @@ int orin_flash_attention_prefill(int32_t start_pos, int32_t seq_len, int32_t hea
  * orin_qk_norm_rope on the query followed by orin_flash_attention_prefill, bit for bit, and
  * the query buffer is left unchanged.  Keys must already be in the cache (orin_qk_norm_rope
  * with query = NULL writes them).  fp16 / bf16, head_size 64 or 128; output must not
- * alias query.
+ * alias query.  bf16 V: the range limits of orin_flash_attention_prefill.
  */
 int orin_flash_attention_prefill_qk_norm_rope(
     int32_t start_pos, int32_t seq_len, int32_t head_num, int32_t kv_head_num, int32_t head_size,
@@ -134,7 +140,8 @@ int orin_flash_attention_prefill_qk_norm_rope(
  * flash_attention2_decode_cu / flash_attention2_decode_fp16_cu
  * (flash_attention_kernel.cuh:50-63, 84-97, 186-216).  One query row [dim] at
  * position pos over cache rows 0..pos.  Split-KV partials go to the stream's
- * library-owned workspace (see orin_attn_workspace_reserve_stream).
+ * library-owned workspace (see orin_attn_workspace_reserve_stream).  bf16 caches: the
+ * weights are split into bf16 hi + lo parts and V is used as stored (bf16's full range).
  */
 int orin_flash_attention_decode(int32_t pos, int32_t head_num, int32_t kv_head_num,
                                 int32_t head_size, int32_t kv_mul, int32_t layer_index,
@@ -221,9 +228,14 @@ int orin_attn_workspace_release(void);
  * cannot see device lengths) gets NaN outputs instead of attention over a truncated
  * prefix; the same holds for *pos_ptr >= max_seq_len in the gpu-pos entry points.
  * split_tokens: tokens per split (multiple of 64, else ORIN_ERR_INVALID_ARG), 0 =
- * automatic (from max_context_len alone; orin_attn_decode_split_tokens_for_total uses the
- * batch's total length too).  Workspace: orin_attn_decode_workspace_size bytes (may be NULL
- * when that is 0).
+ * automatic: whole rows (one split per row, no workspace) when batch * kv_head_num is at
+ * least the device's CU count, else splits sized from max_context_len alone
+ * (orin_attn_decode_split_tokens_for_total uses the batch's total length too).  Launches
+ * of whole rows with batch * kv_head_num >= CUs run the matrix-core kernel where it
+ * supports the shape (16-bit caches, head_size 64 or 128, at most 16 query heads per kv
+ * head); the rest run the dot-product kernel.  Workspace: orin_attn_decode_workspace_size
+ * bytes (may be NULL when that is 0).  bf16 caches: V is used as stored (the weights are
+ * split into bf16 hi + lo parts), so bf16's full range is kept.
  */
 size_t orin_attn_decode_workspace_size(int32_t batch, int32_t head_num, int32_t kv_head_num,
                                        int32_t head_size, int32_t max_context_len,
@@ -233,18 +245,13 @@ int32_t orin_attn_decode_split_tokens(int32_t batch, int32_t head_num, int32_t k
 /*
  * Split size for a batched decode whose total KV length sum_context_len (the sum of the
  * rows' context lengths) the caller knows on the host -- a serving loop keeps it; no
- * reference counterpart.  When every row is close to max_context_len (sum >= 0.9 * batch *
- * max_context_len) the launch gets one split per row when the (row, kv head) units fill
- * the CUs in rounds at least 90% full, else a few long splits per row (one round of the
- * workgroups the device holds at once); both stream faster than the automatic choice.
- * Otherwise it returns the automatic choice.  A launch with one split per row runs one
- * 16-wave (whole-CU) workgroup per (row, kv head, head group) and no merge when K/V are
- * 16-bit and head_size is 128 with at most 4 query heads per kv head, or 64 with at most
- * 3 (fp32: head_size 64, one query head per kv head); the same 16-wave workgroups (then
- * followed by the merge) also run any split launch with no more workgroups than the
- * device has CUs, e.g. batch 1.  Other shapes run 4-wave workgroups, which a near-uniform batch of whole rows does not
- * fill, so pass such callers' automatic split instead.  Pass the result as split_tokens (and to
- * orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid arguments.
+ * reference counterpart.  A batch whose (row, kv head) units reach the CU count gets whole
+ * rows, as the automatic choice does.  A smaller batch whose rows are all close to
+ * max_context_len (sum >= 0.9 * batch * max_context_len) gets a few long splits per row
+ * (one round of the workgroups the device holds at once), which streams faster than the
+ * automatic choice; otherwise the automatic choice.  Pass the result as split_tokens (and
+ * to orin_attn_decode_workspace_size).  Returns a multiple of 64, or 0 for invalid
+ * arguments.
  */
 int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,
                                                 int32_t kv_head_num, int32_t max_context_len,
@@ -287,7 +294,9 @@ int orin_attn_decode_paged(const void* query, const void* k_pool, const void* v_
  * (kuiper/source/op/kernels/cuda/vision_encoder_kernel.cuh:159-170): bidirectional
  * attention of num_tokens tokens over q/k/v [num_heads, num_tokens, head_dim] into
  * output [num_tokens, num_heads*head_dim].  The reference's out_transposed and scores
- * workspaces are not needed and may be NULL.  fp16 / bf16 (MFMA) or fp32.
+ * workspaces are not needed and may be NULL.  fp16 / bf16 (MFMA) or fp32.  bf16 V: the
+ * range limits of orin_flash_attention_prefill (|v| <= 65504; subnormal spacing below
+ * 2^-14).
  */
 int orin_vision_attention_pretransposed(const void* q, const void* k, const void* v,
                                         void* output, void* out_transposed, void* scores,

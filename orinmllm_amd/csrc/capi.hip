@@ -627,17 +627,12 @@ int32_t orin_attn_decode_split_tokens_for_total(int32_t batch, int32_t head_num,
                                                       max_context_len, 0);
   if (max_context_len == 0 || sum_context_len * 10 < (int64_t)batch * max_context_len * 9)
     return automatic;
-  // Near-uniform rows.  When whole rows fill the CUs in rounds that are at least 90% full,
-  // one split per row: the launch then runs one 16-wave workgroup per (row, kv head, head
-  // group), a whole CU each, with no partials and no merge launch (batch 32, 8 kv heads,
-  // 4096 tokens: 90.3-91.5 us against 94.1-94.5 for 1024-token splits).
+  // Near-uniform rows.  A batch with a unit per CU or more already gets whole rows.
   const long base = decode_base_blocks(batch, head_num, kv_head_num);
   const long cus = device_cus();
-  const long rounds = (base + cus - 1) / cus;
-  if (base >= cus && base * 10 >= rounds * cus * 9) return round_up(max_context_len, 64);
-  // Otherwise one round of the 4-wave workgroups resident at once (4 per CU): at batch 32,
-  // 8 kv heads, 4096 tokens that would be 1024-token splits (97.4 us against 100.1 for
-  // 2048 and 102-103 for the automatic 320).
+  if (base >= cus) return automatic;
+  // Otherwise one round of the 4-wave workgroups resident at once (4 per CU), e.g. at
+  // batch 8, 8 kv heads, 4096 tokens 256-token splits.
   long per_row = cus * 4 / base;
   if (per_row < 1) per_row = 1;
   int st = round_up((max_context_len + per_row - 1) / per_row, 64);

@@ -230,6 +230,19 @@ __device__ __forceinline__ float shfl_xor_f(float x, int mask) {
       float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
 }
 
+// x of lane l ^ 32: v_permlane32_swap_b32 on x and a copy of it.  The copy and the swap
+// are one asm block with two wait states between them: on gfx950 a VALU write of a VGPR
+// that v_permlane*_swap then reads needs two wait states, and the compiler's hazard check
+// does not see VGPR writes made inside inline asm (a copy written by a separate asm
+// statement could land right before the swap).  Lanes < 32 find their partner in the swapped
+// copy, lanes >= 32 in the swapped original.
+__device__ __forceinline__ float partner32(float x) {
+  int a = __builtin_bit_cast(int, x), b;
+  __asm__ volatile("v_mov_b32 %1, %0\n\ts_nop 1\n\tv_permlane32_swap_b32 %0, %1"
+                   : "+v"(a), "=&v"(b));
+  return __builtin_bit_cast(float, (__lane_id() < 32) ? b : a);
+}
+
 // Max / sum across the 8 lane groups of a wave (lanes with equal lane%8).
 __device__ __forceinline__ float max_across_groups8(float x) {
   x = fmaxf(x, dpp_mov<kDppRowRor8>(x));

@@ -352,11 +352,10 @@ decode_split_kernel(DecodeArgs a) {
       }
       // Token j = 8s + r of the tile has its weights in lane group r (lane 8r); they are
       // broadcast with v_readlane into scalar registers.
-      if constexpr (sizeof(T) == 2) {
-        // 16-bit K/V: tokens 8(2u)+r and 8(2u+1)+r share one packed weight pair, so one
+      if constexpr (std::is_same<T, f16>::value) {
+        // fp16 K/V: tokens 8(2u)+r and 8(2u+1)+r share one packed weight pair, so one
         // v_dot2 does two tokens.  The weights are rounded to fp16 (as P is in the MFMA
-        // prefill; bf16 V pairs are converted to fp16); the normaliser l keeps the fp32
-        // weights.
+        // prefill); the normaliser l keeps the fp32 weights.
 #pragma unroll
         for (int u = 0; u < STEPS / 2; ++u) {
           uint32_t pw[G];
@@ -367,15 +366,39 @@ decode_split_kernel(DecodeArgs a) {
           for (int r = 0; r < 8; ++r) {
             uint32_t vp[EPL];
             pair_rows<EPL>(vr[16 * u + r], vr[16 * u + 8 + r], vp);
-            if constexpr (!std::is_same<T, f16>::value) {
-#pragma unroll
-              for (int e = 0; e < EPL; ++e) vp[e] = bf16x2_to_f16x2(vp[e]);
-            }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
               const uint32_t p2 = __builtin_amdgcn_readlane(pw[g], r * 8);
 #pragma unroll
               for (int e = 0; e < EPL; ++e) acc[g][e] = dot2<f16>(p2, vp[e], acc[g][e]);
+            }
+          }
+        }
+      } else if constexpr (sizeof(T) == 2) {
+        // bf16 K/V: the same token pairs, with each weight split into bf16 hi + lo (16
+        // significant bits together) and two bf16 v_dot2 per pair, so V is used as stored
+        // and keeps bf16's full range.
+#pragma unroll
+        for (int u = 0; u < STEPS / 2; ++u) {
+          uint32_t ph[G], pl[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float p0 = sc[2 * u][g], p1 = sc[2 * u + 1][g];
+            const bf16 h0 = (bf16)p0, h1 = (bf16)p1;
+            ph[g] = __builtin_bit_cast(uint32_t, bf16x2{h0, h1});
+            pl[g] = __builtin_bit_cast(uint32_t, bf16x2{(bf16)(p0 - (float)h0), (bf16)(p1 - (float)h1)});
+          }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            uint32_t vp[EPL];
+            pair_rows<EPL>(vr[16 * u + r], vr[16 * u + 8 + r], vp);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const uint32_t h2 = __builtin_amdgcn_readlane(ph[g], r * 8);
+              const uint32_t l2 = __builtin_amdgcn_readlane(pl[g], r * 8);
+#pragma unroll
+              for (int e = 0; e < EPL; ++e)
+                acc[g][e] = dot2<bf16>(l2, vp[e], dot2<bf16>(h2, vp[e], acc[g][e]));
             }
           }
         }

@@ -43,9 +43,6 @@
 #include "common.h"
 #include "kernels.h"
 
-#include <stdlib.h>
-#include <string.h>
-
 namespace orin {
 
 namespace {
@@ -113,17 +110,6 @@ __device__ __forceinline__ float sum_pair<bf16>(uint32_t p, float acc) {
                                          bf16x2{(bf16)1.0f, (bf16)1.0f}, acc, false);
 }
 
-// x of lane l^32.  v_permlane32_swap exchanges the upper half of its first operand
-// with the lower half of its second; with both holding x, one result has x[l^32] in
-// the lower lanes and the other in the upper lanes.  The second operand is an opaque
-// copy: this toolchain folds permlane32_swap(x, x) to {x, x}, which is wrong for the
-// lanes that should receive the other half.
-__device__ __forceinline__ float partner32(float x) {
-  int y;
-  __asm__("v_mov_b32 %0, %1" : "=v"(y) : "v"(__builtin_bit_cast(int, x)));
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), y, false, false);
-  return __builtin_bit_cast(float, (__lane_id() < 32) ? r[1] : r[0]);
-}
 // Max / sum of x over lanes l and l^32 (every lane gets the result).
 __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, partner32(x)); }
 __device__ __forceinline__ float pair_sum(float x) { return x + partner32(x); }
@@ -478,19 +464,11 @@ hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
 
 // Head sizes 64-128 go to the ping-pong kernel (256-query workgroups, one per CU) when its
 // grid covers every CU at least once, or when the caller planned a key split for a causal
-// launch that does not (fwd_pp_key_split).  ORIN_FWD_KERNEL=tile|pp overrides the choice (for
-// measurements and tests); unset or any other value keeps it.
+// launch that does not (fwd_pp_key_split).
 template <bool CAUSAL>
 bool use_pp(const FwdArgs& a, int dtype) {
-  static const int mode = [] {
-    const char* e = getenv("ORIN_FWD_KERNEL");
-    if (!e) return -1;
-    if (!strcmp(e, "tile")) return 0;
-    if (!strcmp(e, "pp")) return 1;
-    return -1;
-  }();
-  if (mode == 0 || !fwd_pp_supports(a, dtype)) return false;
-  if (mode == 1 || (CAUSAL && (a.key_chunk_tiles > 0 || a.rope_sin))) return true;
+  if (!fwd_pp_supports(a, dtype)) return false;
+  if (CAUSAL && (a.key_chunk_tiles > 0 || a.rope_sin)) return true;
   const long blocks = CAUSAL ? (long)((a.n_q + 255) / 256) * a.Hq
                              : (long)a.n_seg * ((a.max_seqlen + 255) / 256) * a.Hq;
   return blocks >= 256;

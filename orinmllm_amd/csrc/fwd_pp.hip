@@ -44,37 +44,6 @@
 
 #include <type_traits>
 
-#ifdef ORIN_PP_TIMELINE
-// Timeline build (orinmllm_amd/microbench/prefill_timeline.hip only; the library never
-// defines it): per workgroup, wave 0 stamps the 100 MHz wall clock at [0] entry, [1] first
-// K/V stage landed, [2] main-loop entry, and each wave w at [3 + w] the end of its tiles;
-// [11] = tiles, [12] = shader clocks of wave 0 from entry to [3].
-__device__ unsigned long long orin_pp_timeline[8192 * 16];
-#define PP_STAMP(i, cond)                                                         \
-  do {                                                                            \
-    if ((cond) && lane == 0 && blockIdx.x < 8192)                                 \
-      orin_pp_timeline[(long)blockIdx.x * 16 + (i)] = wall_clock64();             \
-  } while (0)
-// Steps kStepStamp0 .. +3 of waves 0 (group 0) and 4 (group 1), which share a SIMD: shader
-// clock at [0] the step's start, [1] the end of the wave's phase work (its last MFMA or
-// softmax instruction issued), [2] the step's exit from the barrier.
-constexpr int kStepStamp0 = 12;
-__device__ unsigned long long orin_pp_steps[8192 * 2 * 4 * 3];
-#define PP_STEP_STAMP(k, j)                                                                \
-  do {                                                                                     \
-    if (lane == 0 && (wave & 3) == 0 && (k) >= kStepStamp0 && (k) < kStepStamp0 + 4 &&    \
-        blockIdx.x < 8192)                                                                 \
-      orin_pp_steps[(((long)blockIdx.x * 2 + (wave >> 2)) * 4 + (k) - kStepStamp0) * 3 + (j)] = \
-          clock64();                                                                       \
-  } while (0)
-#else
-#define PP_STAMP(i, cond) \
-  do {                    \
-  } while (0)
-#define PP_STEP_STAMP(k, j) \
-  do {                      \
-  } while (0)
-#endif
 
 namespace orin {
 
@@ -95,10 +64,7 @@ constexpr int pp_lds_bytes() { return 2 * pp_stages<T>() * PTILE_BYTES; }  // 96
 constexpr int kXcdsPP = 8;
 // A lane's 32 weights of one tile may sum to at most this before the row maximum is raised.
 constexpr float kTileSumMax = 256.0f;
-#ifndef PP_PF
-#define PP_PF 3
-#endif
-constexpr int PF = PP_PF;  // LDS reads run this many MFMAs ahead of their use
+constexpr int PF = 3;  // LDS reads run this many MFMAs ahead of their use
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -136,13 +102,6 @@ __device__ __forceinline__ float sum_pair<bf16>(uint32_t p, float acc) {
                                          bf16x2{(bf16)1.0f, (bf16)1.0f}, acc, false);
 }
 
-// x of lane l^32 (see fwd.hip: the second operand must be an opaque copy).
-__device__ __forceinline__ float partner32(float x) {
-  int y;
-  __asm__("v_mov_b32 %0, %1" : "=v"(y) : "v"(__builtin_bit_cast(int, x)));
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), y, false, false);
-  return __builtin_bit_cast(float, (__lane_id() < 32) ? r[1] : r[0]);
-}
 
 // s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
 template <int N>
@@ -172,9 +131,11 @@ __device__ __forceinline__ void step_barrier() {
 // One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): lane l's data
 // lands at LDS byte lds_addr + 16 l.  Issued from inline asm so that the compiler does
 // not treat it as an LDS store to wait for before every later LDS read: the kernel
-// orders these transfers itself (vmcnt wait + barrier before the stage is read).
+// orders these transfers itself (vmcnt wait + barrier before the stage is read).  An LDS
+// DMA that reads M0 right after an SALU write of M0 needs one wait state on gfx9-family
+// parts, which the compiler cannot insert inside the asm: hence the s_nop.
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
-  __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+  __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                    :
                    : "v"(gptr), "s"(lds_addr)
                    : "memory", "m0");
@@ -183,7 +144,7 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
 // The same transfer from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset:
 // the per-tile address arithmetic stays on the scalar unit.
 __device__ __forceinline__ void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
-  __asm__ volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                    :
                    : "v"(voff), "s"(sbase), "s"(lds_addr)
                    : "memory", "m0");
@@ -400,15 +361,8 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-#ifndef PP_GRP
-#define PP_GRP 0
-#endif
-  const int grp = PP_GRP == 0 ? (wave >> 2) : (wave & 1);
+  const int grp = wave >> 2;
   const int lq = lane & 31, hf = lane >> 5;
-#ifdef ORIN_PP_TIMELINE
-  const unsigned long long tl_c0 = clock64();
-#endif
-  PP_STAMP(0, wave == 0);
 
   // ------------------------------------------------------------ block -> (head, rows)
   int head, q_lo, q_n, seg_start, kv_end, pos_off;
@@ -467,7 +421,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
 
   // Row slots interleave the groups (group 0: slots 0,2,4,6; group 1: 1,3,5,7) so both
   // groups reach the causal diagonal in the same tiles.
-  const int slot = PP_GRP == 0 ? 2 * (wave & 3) + grp : wave;
+  const int slot = 2 * (wave & 3) + grp;
   const int wq0 = q_lo + 32 * slot;
   const int qi = wq0 + lq;
   const int wpos0 = pos_off + wq0;
@@ -567,7 +521,6 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
   wait_stage(min(n_tiles, PSTAGES - 1));
   step_barrier();
-  PP_STAMP(1, wave == 0);
 
   f32x16 oacc[DT];
 #pragma unroll
@@ -787,25 +740,18 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // the QK product of the next tile, also for a wave whose queries all precede it: one
   // MFMA-phase shape inside the loop keeps the accumulators in fixed registers.
   auto tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
-    PP_STEP_STAMP(k, 0);
     step_begin(k);
     __builtin_amdgcn_s_setprio(1);
     if (active(t)) mphase(slot_tag, std::true_type{});
     __builtin_amdgcn_s_setprio(0);
-    PP_STEP_STAMP(k, 1);
     step_end(k);
     ++k;
-    PP_STEP_STAMP(k - 1, 2);
-    PP_STEP_STAMP(k, 0);
     step_begin(k);
     if (active(t + 1)) softmax(t + 1);
-    PP_STEP_STAMP(k, 1);
     step_end(k);
     ++k;
-    PP_STEP_STAMP(k - 1, 2);
   };
   const int n_loop = n_tiles - 1;
-  PP_STAMP(2, wave == 0);
   for (int t = 0; t < n_loop; t += PSTAGES) {
     tile(t, std::integral_constant<int, 1>{});
     if (t + 1 < n_loop) tile(t + 1, std::integral_constant<int, 2>{});
@@ -835,13 +781,6 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 
   // ------------------------------------------------------------ normalise and store
-  PP_STAMP(3 + wave, true);
-#ifdef ORIN_PP_TIMELINE
-  if (lane == 0 && wave == 0 && blockIdx.x < 8192) {
-    orin_pp_timeline[(long)blockIdx.x * 16 + 11] = (unsigned long long)n_tiles;
-    orin_pp_timeline[(long)blockIdx.x * 16 + 12] = clock64() - tl_c0;
-  }
-#endif
   const float l_tot = l_run + partner32(l_run);
   const float inv = 1.f / l_tot;
   if (partial) {
