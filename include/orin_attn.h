@@ -202,9 +202,17 @@ size_t orin_flash_attention_decode_noalloc_max_bytes(void);
  * causal prefill launch (0 when it does not split).  orin_attn_workspace_reserve_stream
  * allocates both on the current device for `stream` now.  orin_attn_workspace_reserve
  * reserves decode bytes for the NULL stream and makes every decode buffer created later on
- * this device at least that large.  orin_attn_workspace_release synchronises the device and
- * frees every library-owned buffer of the current device; call it only when no captured
- * graph that used them will be replayed.
+ * this device at least that large.  orin_attn_workspace_reserve_stream also prepares the
+ * device's output-projection handle (orin_batched_matmul), so that it can be captured.
+ *  - Buffers are keyed by (device, stream handle) and live until released: a stream that is
+ *    destroyed keeps its buffers (and a new stream that receives the same handle value
+ *    reuses them).  orin_attn_workspace_release_stream(stream) synchronises `stream` and
+ *    frees its buffers on the current device; orin_attn_workspace_release synchronises the
+ *    device and frees every library-owned buffer of it.  Call either only when no captured
+ *    graph that used those buffers will be replayed; both return ORIN_ERR_WORKSPACE, and
+ *    free nothing, while one of the affected streams is being captured.
+ *  - Allocations are made with the calling thread in relaxed capture mode, so they do not
+ *    invalidate a capture that another thread runs in global mode.
  */
 size_t orin_flash_attention_decode_workspace_size(int32_t head_num, int32_t head_size,
                                                   int32_t max_seq_len);
@@ -214,6 +222,7 @@ size_t orin_flash_attention_prefill_workspace_size(int32_t start_pos, int32_t se
 int orin_attn_workspace_reserve(size_t bytes);
 int orin_attn_workspace_reserve_stream(size_t decode_bytes, size_t prefill_bytes, void* stream);
 int orin_attn_workspace_release(void);
+int orin_attn_workspace_release_stream(void* stream);
 
 /* ------------------------------------------------------------------ batched decode */
 
@@ -325,8 +334,9 @@ int orin_vision_attention_varlen(const void* q, const void* k, const void* v, vo
  * input [batch_size, in_dim] (the attention output [tokens, head_num*head_size], as the
  * attention entry points store it), weight [out_dim, in_dim], output [batch_size, out_dim],
  * all row-major in `dtype` (fp32 / fp16 / bf16); fp32 accumulation.  A plain GEMM, run by
- * rocBLAS on `stream`.  The first call on a device creates its rocBLAS handle (not under
- * graph capture).
+ * rocBLAS on `stream`.  The device's rocBLAS handle and its workspace are created by
+ * orin_attn_workspace_reserve_stream or by the first call outside graph capture; a call on
+ * a capturing stream of a device without them returns ORIN_ERR_WORKSPACE.
  */
 int orin_batched_matmul(const void* input, const void* weight, void* output, int32_t batch_size,
                         int32_t in_dim, int32_t out_dim, float scale, int32_t dtype,

@@ -43,6 +43,7 @@ SIGNATURES = {
     "orin_attn_workspace_reserve": (C.c_int, [sz]),
     "orin_attn_workspace_reserve_stream": (C.c_int, [sz, sz, vp]),
     "orin_attn_workspace_release": (C.c_int, []),
+    "orin_attn_workspace_release_stream": (C.c_int, [vp]),
     "orin_attn_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "orin_attn_decode_split_tokens": (i32, [i32, i32, i32, i32, i32]),
     "orin_attn_decode_split_tokens_for_total": (i32, [i32, i32, i32, i32, i64]),

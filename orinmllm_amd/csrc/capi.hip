@@ -95,7 +95,12 @@ struct WsSlot {
 
 std::mutex g_ws_mu;
 std::vector<WsSlot> g_ws;                          // live buffers
-std::vector<std::pair<int, void*>> g_ws_retired;   // (device, buffer) kept for graphs
+struct WsRetired {
+  int dev;
+  void* stream;
+  void* ptr;
+};
+std::vector<WsRetired> g_ws_retired;               // grown-out buffers kept for graphs
 std::vector<size_t> g_ws_floor;                    // per device: minimum decode buffer size
 
 // Grow geometrically so that a sequence of slightly larger calls retires few buffers.
@@ -103,6 +108,25 @@ size_t grown_size(size_t have, size_t need) {
   size_t n = have ? have : 1;
   while (n < need) n *= 2;
   return n < need ? need : n;
+}
+
+// hipMalloc with this thread in relaxed capture mode: a stream that another thread is
+// capturing in global mode is then not invalidated by the allocation.
+hipError_t relaxed_malloc(void** p, size_t bytes) {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
+  if (e != hipSuccess) return e;
+  e = hipMalloc(p, bytes);
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  return e;
+}
+
+// True when `stream` is being captured (the null stream never is).
+bool capturing(void* stream) {
+  if (!stream) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess &&
+         cs != hipStreamCaptureStatusNone;
 }
 
 int library_workspace(int kind, hipStream_t stream, size_t bytes, void** out) {
@@ -131,10 +155,10 @@ int library_workspace(int kind, hipStream_t stream, size_t bytes, void** out) {
   if (kind == kWsDecode && dev < (int)g_ws_floor.size() && g_ws_floor[dev] > want)
     want = g_ws_floor[dev];
   void* p = nullptr;
-  e = hipMalloc(&p, want);
+  e = relaxed_malloc(&p, want);
   if (e != hipSuccess) return hip_status(e);
   if (slot) {
-    g_ws_retired.push_back({dev, slot->ptr});
+    g_ws_retired.push_back({dev, slot->stream, slot->ptr});
     slot->ptr = p;
     slot->bytes = want;
   } else {
@@ -230,18 +254,28 @@ int orin_attn_workspace_reserve_stream(size_t decode_bytes, size_t prefill_bytes
   void* p;
   int st = library_workspace(kWsDecode, (hipStream_t)stream, decode_bytes, &p);
   if (st != ORIN_OK) return st;
-  return library_workspace(kWsPrefillSplit, (hipStream_t)stream, prefill_bytes, &p);
+  st = library_workspace(kWsPrefillSplit, (hipStream_t)stream, prefill_bytes, &p);
+  if (st != ORIN_OK) return st;
+  // The output projection's rocBLAS handle and workspace, so that a capture of it on this
+  // device allocates nothing.
+  return output_projection_prepare() == 0 ? ORIN_OK : ORIN_ERR_LAUNCH;
 }
 
-int orin_attn_workspace_release(void) {
+// Frees the library-owned buffers of the current device that belong to `stream` (all
+// streams when all_streams), after synchronising what may still use them.  Refused while
+// one of those streams is being captured.
+static int release_buffers(bool all_streams, void* stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_status(e);
-  e = hipDeviceSynchronize();
-  if (e != hipSuccess) return hip_status(e);
   std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto mine = [&](int d, void* s) { return d == dev && (all_streams || s == stream); };
+  for (const auto& w : g_ws)
+    if (mine(w.dev, w.stream) && capturing(w.stream)) return ORIN_ERR_WORKSPACE;
+  e = all_streams ? hipDeviceSynchronize() : hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_status(e);
   for (auto it = g_ws.begin(); it != g_ws.end();) {
-    if (it->dev == dev) {
+    if (mine(it->dev, it->stream)) {
       (void)hipFree(it->ptr);
       it = g_ws.erase(it);
     } else {
@@ -249,16 +283,20 @@ int orin_attn_workspace_release(void) {
     }
   }
   for (auto it = g_ws_retired.begin(); it != g_ws_retired.end();) {
-    if (it->first == dev) {
-      (void)hipFree(it->second);
+    if (mine(it->dev, it->stream)) {
+      (void)hipFree(it->ptr);
       it = g_ws_retired.erase(it);
     } else {
       ++it;
     }
   }
-  if (dev < (int)g_ws_floor.size()) g_ws_floor[dev] = 0;
+  if (all_streams && dev < (int)g_ws_floor.size()) g_ws_floor[dev] = 0;
   return ORIN_OK;
 }
+
+int orin_attn_workspace_release(void) { return release_buffers(true, nullptr); }
+
+int orin_attn_workspace_release_stream(void* stream) { return release_buffers(false, stream); }
 
 // ------------------------------------------------------------------ fp32 MHA
 
@@ -835,8 +873,9 @@ int orin_batched_matmul(const void* input, const void* weight, void* output, int
     return ORIN_ERR_INVALID_ARG;
   if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return ORIN_ERR_UNSUPPORTED;
   const int st = output_projection(input, weight, output, batch_size, in_dim, out_dim, scale,
-                                   dtype, (hipStream_t)stream);
+                                   dtype, (hipStream_t)stream, capturing(stream));
   if (st == -2) return ORIN_ERR_UNSUPPORTED;
+  if (st == -3) return ORIN_ERR_WORKSPACE;
   if (st != 0) {
     g_last_hip_error = "rocBLAS gemm_ex failed";
     return ORIN_ERR_LAUNCH;

@@ -115,8 +115,11 @@ hipError_t launch_vision_qkv(const void* qkv, const void* cos_t, const void* sin
                              void* k, void* v, int N, int H, int d, int dtype, hipStream_t stream);
 
 // Attention output projection (outproj.hip): out[b, k] = scale * sum_m in[b, m] * w[k, m].
-// Returns 0, -1 (library error) or -2 (dtype).
+// Returns 0, -1 (library error), -2 (dtype) or -3 (the stream is capturing and the device's
+// handle was not prepared).
 int output_projection(const void* input, const void* weight, void* output, int batch, int in_dim,
-                      int out_dim, float scale, int dtype, hipStream_t stream);
+                      int out_dim, float scale, int dtype, hipStream_t stream, bool capturing);
+// Creates the current device's rocBLAS handle and its workspace if missing (0 on success).
+int output_projection_prepare();
 
 }  // namespace orin

@@ -59,3 +59,29 @@ def test_batched_matmul_argument_errors():
                                    _lib.DTYPE_FP16, s) == _lib.ERR_INVALID_ARG
     assert lib.orin_batched_matmul(x.data_ptr(), x.data_ptr(), x.data_ptr(), 4, 8, 8, 1.0, 7,
                                    s) == _lib.ERR_UNSUPPORTED
+
+
+def test_output_projection_graph_capture():
+    """After orin_attn_workspace_reserve_stream (which prepares the device's rocBLAS handle
+    and workspace) the projection can be captured: every replay, with new inputs written
+    eagerly between replays, equals an eager call."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    B, n = 32, 4096  # the decode step's wo: 32 rows x 4096 -> 4096
+    x = torch.randn(B, n, device="cuda", generator=g).half()
+    w = (torch.randn(n, n, device="cuda", generator=g) / n ** 0.5).half()
+    out = torch.full((B, n), float("nan"), device="cuda", dtype=torch.float16)
+    cap = torch.cuda.Stream()
+    K.reserve_decode_workspace(32, 128, 4096, stream=cap)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        K.batched_matmul_kernel_cu(x, w, out, B, 1.0, config=K.CudaConfig(cap))
+    for i in range(3):
+        x.copy_(torch.randn(B, n, device="cuda", generator=g).half())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = torch.empty_like(out)
+        K.batched_matmul_kernel_cu(x, w, eager, B, 1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"

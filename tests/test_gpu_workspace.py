@@ -189,3 +189,37 @@ def test_device_length_past_launch_bound_is_nan():
     dec.gpu_pos(out, torch.cuda.current_stream())
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
+
+
+def test_release_stream():
+    """orin_attn_workspace_release_stream frees one stream's buffers (a later call on that
+    stream allocates again and gives the same bits) and is refused, freeing nothing, while
+    that stream is being captured; orin_attn_workspace_release is refused likewise."""
+    rng = np.random.default_rng(34)
+    dec = Decode(rng)
+    lib = _lib.load()
+    s = torch.cuda.Stream()
+    first, again = dec.new_out(), dec.new_out()
+    dec.host_pos(3000, first, s)
+    torch.cuda.synchronize()
+    assert lib.orin_attn_workspace_release_stream(C.c_void_p(s.cuda_stream)) == _lib.OK
+    dec.host_pos(3000, again, s)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    K.reserve_decode_workspace(dec.Hq, dec.d, dec.max_seq, stream=s)
+    out = dec.new_out()
+    g = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.graph(g, stream=s):
+        dec.gpu_pos(out, s)
+        status.append(lib.orin_attn_workspace_release_stream(C.c_void_p(s.cuda_stream)))
+        status.append(lib.orin_attn_workspace_release())
+    assert status == [_lib.ERR_WORKSPACE, _lib.ERR_WORKSPACE]
+    dec.pos.fill_(3000)
+    torch.cuda.synchronize()
+    g.replay()  # the buffers survived the refused releases
+    torch.cuda.synchronize()
+    assert torch.equal(out, first)
+    del g
+    torch.cuda.synchronize()
+    assert lib.orin_attn_workspace_release_stream(C.c_void_p(s.cuda_stream)) == _lib.OK
