@@ -350,6 +350,38 @@ def time_fused_pipeline(K, dtype, gen, reps=50):
             "wo_projection_TFLOP/s": round(wo_tflops, 1)}
 
 
+def time_decode_pipeline(K, dtype, gen, dc, ws, pools, reps=50):
+    """The C4 decode step followed by its wo projection (kuiper/source/model/qwen_base.cpp:
+    464-474): attention output [32, 4096] x wo [4096, 4096]^T.  Median per-launch times of
+    the decode, of the projection, and of the two back to back in one event pair; the
+    projection is bound by reading wo (32 MB), the attention output round trip between the
+    two launches is 2 x 256 KB."""
+    import torch
+    B, n = dc["B"], dc["Hq"] * dc["d"]
+    wo = (torch.randn(n, n, device="cuda", generator=gen) / n ** 0.5).to(dtype)
+    y = torch.empty(B, n, device="cuda", dtype=dtype)
+    stream = torch.cuda.current_stream()
+
+    def dec(i):
+        p = i % pools
+        K.paged_decode_cu(dc["q"], dc["kp"][p], dc["vp"][p], dc["o"], dc["bt"], dc["lens_d"],
+                          dc["maxlen"], workspace=ws, layout=dc["layout"])
+
+    def proj():
+        K.batched_matmul_kernel_cu(dc["o"].view(B, n), wo, y, B)
+
+    def both(i):
+        dec(i)
+        proj()
+
+    t_dec = per_launch(dec, reps, 10, stream, indexed=True)["median_ms"] * 1e3
+    t_proj = per_launch(proj, reps, 10, stream)["median_ms"] * 1e3
+    t_both = per_launch(both, reps, 10, stream, indexed=True)["median_ms"] * 1e3
+    return {"decode_us": round(t_dec, 2), "wo_us": round(t_proj, 2), "decode_then_wo_us": round(t_both, 2),
+            "wo_GB/s": round(2 * n * n / (t_proj * 1e-6) / 1e9, 1),
+            "attn_out_roundtrip_bytes": 2 * B * n * 2}
+
+
 def cpu_baseline(pf, dc, min_seconds=8.0):
     """Time the oracle (all host cores, OpenMP over query rows) on the full C3 prefill and
     the full C4 decode, repeating each until it has run about min_seconds."""
@@ -527,6 +559,8 @@ def main():
         out["other_configs"] = time_other_configs(K, gen)
     if not args.no_producers and not args.no_pipeline:
         out["c3_pipeline"] = time_fused_pipeline(K, dtype, gen)
+    if not args.no_pipeline:
+        out["decode_pipeline"] = time_decode_pipeline(K, dtype, gen, dc, ws, args.pools)
     if not args.no_producers:
         out["producers"] = time_producers(K, make_producers(dtype, gen))
         for name, rec in out["producers"].items():

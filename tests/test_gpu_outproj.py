@@ -85,3 +85,47 @@ def test_output_projection_graph_capture():
         K.batched_matmul_kernel_cu(x, w, eager, B, 1.0)
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("batch,in_dim,out_dim", [(1, 4096, 4096), (7, 1536, 1536), (16, 512, 16),
+                                                  (32, 4096, 4096), (33, 1536, 4096),
+                                                  (64, 2048, 1024)])
+def test_decode_rows_projection_vs_fp64(kind, batch, in_dim, out_dim):
+    """Decode-sized batches (one token per sequence): against a float64 matmul of the same
+    16-bit inputs, within the lowp bar."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(batch * 7 + in_dim + out_dim)
+    x = torch.randn(batch, in_dim, device="cuda", generator=g).to(TORCH[kind])
+    w = (torch.randn(out_dim, in_dim, device="cuda", generator=g) / in_dim ** 0.5).to(TORCH[kind])
+    out = torch.full((batch, out_dim), float("nan"), device="cuda", dtype=TORCH[kind])
+    K.batched_matmul_kernel_cu(x, w, out, batch, 0.75)
+    torch.cuda.synchronize()
+    ref = 0.75 * (x.double().cpu().numpy() @ w.double().cpu().numpy().T)
+    assert_lowp_close(out.float().cpu().numpy(), ref, what=f"decode wo {kind} {batch}x{in_dim}x{out_dim}")
+
+
+def test_decode_step_then_projection_vs_oracle():
+    """The C4 decode step (batch 32, Qwen3 heads, paged fp16 pool) followed by its wo: the
+    oracle's decode output multiplied by wo in float64 is the reference."""
+    from oracle import oracle
+    from tests.test_gpu_decode import make_paged
+    from tests.util import normal, quantize
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, d, bs = 32, 32, 8, 128, 16
+    lens = rng.integers(1, 900, B).astype(np.int32)
+    kc, vc, kp, vp, bt = make_paged(rng, lens, Hkv, d, bs, "fp16")
+    q = quantize(normal(rng, (B, Hq, d)), "fp16")
+    w = quantize(normal(rng, (Hq * d, Hq * d)) / np.float32(np.sqrt(Hq * d)), "fp16")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", torch.float16)
+    attn = torch.empty(B, Hq, d, device="cuda", dtype=torch.float16)
+    K.paged_decode_cu(dev(q), dev(kp), dev(vp), attn, torch.from_numpy(bt).cuda(),
+                      torch.from_numpy(lens).cuda(), int(lens.max()),
+                      layout=K.KV_LAYOUT_TOKEN_MAJOR)
+    y = torch.empty(B, Hq * d, device="cuda", dtype=torch.float16)
+    K.batched_matmul_kernel_cu(attn.view(B, Hq * d), dev(w), y, B)
+    torch.cuda.synchronize()
+    ref_attn = oracle.decode_contig(q, kc, vc, lens).reshape(B, Hq * d)
+    ref = ref_attn.astype(np.float64) @ w.astype(np.float64).T
+    # the decode output is rounded to fp16 before the projection: bound that rounding too
+    assert_lowp_close(y.float().cpu().numpy(), ref, atol=4e-3, rtol=2e-2, what="decode + wo")
