@@ -95,3 +95,32 @@ def test_whole_row_decode_bf16_range(scale):
     ref = oracle.decode_contig(q, kc, vc, lens)
     # the lowp bar on values rescaled to unit size
     assert_lowp_close(got / scale, ref / scale, what=f"bf16 V x {scale:g}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_long_whole_rows_repeatable(kind, layout):
+    """Rows of up to 3000 tokens (lengths on and around 32-token tile edges); five launches,
+    with launches of a batch twice as large in between, give the same bits, equal between
+    paged and contiguous caches and within the lowp bar of the oracle."""
+    rng = np.random.default_rng(500 + layout)
+    Hq, Hkv, d, bs = 32, 8, 128, 16
+    B = _batch(Hkv)
+    lens = rng.integers(1, 3001, B).astype(np.int32)
+    lens[:10] = [3000, 1536, 1537, 1538, 1600, 1601, 2047, 2048, 2049, 1]
+    kc, vc, kp, vp, bt = make_paged(rng, lens, Hkv, d, bs, kind)
+    q = quantize(normal(rng, (B, Hq, d)), kind)
+    first = _run(rng, kind, Hq, Hkv, d, bs, layout, lens, q, kc, vc, kp, vp, bt)
+    ref = oracle.decode_contig(q, kc, vc, lens, nthreads=8)
+    assert_lowp_close(first, ref, what=f"long whole rows {kind} layout {layout}")
+    B2 = 2 * B
+    lens2 = rng.integers(1, 2500, B2).astype(np.int32)
+    kc2, vc2, kp2, vp2, bt2 = make_paged(rng, lens2, Hkv, d, bs, kind)
+    q2 = quantize(normal(rng, (B2, Hq, d)), kind)
+    for rep in range(4):
+        got2 = _run(rng, kind, Hq, Hkv, d, bs, layout, lens2, q2, kc2, vc2, kp2, vp2, bt2)
+        again = _run(rng, kind, Hq, Hkv, d, bs, layout, lens, q, kc, vc, kp, vp, bt)
+        assert np.array_equal(again, first), f"repeat {rep}: whole-row decode not reproducible"
+    ref2 = oracle.decode_contig(q2, kc2, vc2, lens2, nthreads=8)
+    assert_lowp_close(got2, ref2, what=f"long whole rows, batch {B2}")
