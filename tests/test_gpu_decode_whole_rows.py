@@ -124,3 +124,71 @@ def test_long_whole_rows_repeatable(kind, layout):
         assert np.array_equal(again, first), f"repeat {rep}: whole-row decode not reproducible"
     ref2 = oracle.decode_contig(q2, kc2, vc2, lens2, nthreads=8)
     assert_lowp_close(got2, ref2, what=f"long whole rows, batch {B2}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layout", [0, 1])
+def test_whole_rows_row_past_bound_is_nan(layout):
+    """A device length above max_context_len makes that row NaN (every head); the other
+    rows of the launch keep the oracle's accuracy."""
+    rng = np.random.default_rng(610 + layout)
+    Hq, Hkv, d, bs = 32, 8, 128, 16
+    B = _batch(Hkv)
+    lens = rng.integers(1, 900, B).astype(np.int32)
+    kc, vc, kp, vp, bt = make_paged(rng, lens, Hkv, d, bs, "fp16")
+    q = quantize(normal(rng, (B, Hq, d)), "fp16")
+    bound = int(np.sort(lens)[-3])
+    bad = lens > bound
+    kpl, vpl = (kp, vp) if layout == K.KV_LAYOUT_TOKEN_MAJOR else (
+        kp.transpose(0, 2, 1, 3), vp.transpose(0, 2, 1, 3))
+    o = torch.zeros(B, Hq, d, device="cuda", dtype=torch.float16)
+    K.paged_decode_cu(dev(q, "fp16"), dev(kpl, "fp16"), dev(vpl, "fp16"), o,
+                      torch.from_numpy(bt).cuda(), torch.from_numpy(lens).cuda(), bound,
+                      split_tokens=(bound + 63) // 64 * 64, layout=layout)
+    torch.cuda.synchronize()
+    got = host(o)
+    assert np.isnan(got[bad]).all()
+    ok = ~bad
+    ref = oracle.decode_contig(q[ok], kc[ok], vc[ok], lens[ok], nthreads=8)
+    assert_lowp_close(got[ok], ref, what="rows within the bound")
+
+
+@pytest.mark.gpu
+def test_whole_rows_graph_replay():
+    """The automatic split's whole-row launch captured in a graph: replays with new
+    lengths and queries written in place give the bits of the eager launch."""
+    rng = np.random.default_rng(620)
+    Hq, Hkv, d, bs = 32, 8, 128, 16
+    B = _batch(Hkv)
+    cap_len = 1024
+    lens = rng.integers(1, cap_len + 1, B).astype(np.int32)
+    kc, vc, kp, vp, bt = make_paged(rng, np.full(B, cap_len, np.int32), Hkv, d, bs, "fp16")
+    dkp = dev(kp.transpose(0, 2, 1, 3), "fp16")
+    dvp = dev(vp.transpose(0, 2, 1, 3), "fp16")
+    dbt = torch.from_numpy(bt).cuda()
+    dlens = torch.from_numpy(lens).cuda()
+    q = quantize(normal(rng, (B, Hq, d)), "fp16")
+    dq = dev(q, "fp16")
+    s = torch.cuda.Stream()
+    out = torch.empty(B, Hq, d, device="cuda", dtype=torch.float16)
+    with torch.cuda.stream(s):
+        K.paged_decode_cu(dq, dkp, dvp, out, dbt, dlens, cap_len, layout=1)  # warm-up
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        K.paged_decode_cu(dq, dkp, dvp, out, dbt, dlens, cap_len, layout=1)
+    for rep in range(3):
+        lens2 = rng.integers(1, cap_len + 1, B).astype(np.int32)
+        q2 = quantize(normal(rng, (B, Hq, d)), "fp16")
+        dlens.copy_(torch.from_numpy(lens2))
+        dq.copy_(dev(q2, "fp16"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(out)
+        eager = torch.empty_like(out)
+        K.paged_decode_cu(dq, dkp, dvp, eager, dbt, dlens, cap_len, layout=1)
+        torch.cuda.synchronize()
+        assert np.array_equal(got, host(eager)), f"replay {rep} differs from the eager launch"
+        ref = oracle.decode_contig(q2, kc, vc, lens2, nthreads=8)
+        assert_lowp_close(got, ref, what=f"replay {rep}")
