@@ -1,9 +1,10 @@
 """Whole-row decode launches that fill the device (at least one (row, kv head) per CU, one
-split per row): the matrix-core decode kernel (decode_mfma.hip).  Every case goes through
-the C ABI, is checked against the oracle and, bit for bit, between the paged pool (both
-layouts, several block sizes) and the contiguous cache.  Lengths include empty rows, one
-key, and lengths on and around the 32-token tile edges; the GQA ratios cover one to
-sixteen query heads per kv head; bf16 values far outside fp16's range must stay exact."""
+split per row): the matrix-core decode kernel (decode_mfma.hip), or the dot-product kernel
+beyond 16 query heads per kv head.  Every case goes through the C ABI, is checked against
+the oracle and, bit for bit, between the paged pool (both layouts, several block sizes) and
+the contiguous cache.  Lengths include empty rows, one key, and lengths on and around the
+32-token tile edges; the GQA ratios cover one to 32 query heads per kv head; bf16 values far
+outside fp16's range must stay exact."""
 import numpy as np
 import pytest
 import torch
@@ -56,6 +57,7 @@ def _run(rng, kind, Hq, Hkv, d, bs, layout, lens, q, kc, vc, kp, vp, bt):
     (64, 4, 128, 64, 0),   # 16 query heads per kv head
     (16, 16, 64, 16, 1),   # MHA, head size 64
     (24, 8, 64, 8, 1),     # 3 per kv head, head size 64
+    (64, 2, 128, 16, 1),   # 32 per kv head: beyond the matrix-core kernel, dot-product kernel
 ])
 def test_whole_row_decode(kind, Hq, Hkv, d, bs, layout):
     rng = np.random.default_rng(Hq * 1000 + Hkv * 10 + d + bs)
