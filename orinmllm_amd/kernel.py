@@ -226,6 +226,19 @@ def reserve_decode_workspace(head_num, head_size, max_seq_len, stream=None, pref
                lib.orin_attn_workspace_reserve_stream(n, prefill_bytes, s))
 
 
+def release_workspace(stream=None, all_streams=False):
+    """Free the library-owned buffers of `stream` (a torch.cuda.Stream; None = the current
+    stream), or of every stream of the current device with all_streams, after synchronising
+    what may still use them; call it before destroying a stream that ran these kernels.
+    Raises while one of those streams is being captured."""
+    lib = _lib.load()
+    if all_streams:
+        _lib.check("orin_attn_workspace_release", lib.orin_attn_workspace_release())
+        return
+    s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
+    _lib.check("orin_attn_workspace_release_stream", lib.orin_attn_workspace_release_stream(s))
+
+
 def prefill_workspace_size(start_pos, seq_len, head_num, kv_head_num, head_size, dtype):
     """Bytes of the library-owned key-split workspace one causal prefill launch needs."""
     return int(_lib.load().orin_flash_attention_prefill_workspace_size(

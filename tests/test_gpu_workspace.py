@@ -226,4 +226,10 @@ def test_release_stream():
     assert torch.equal(out, first)
     del g
     torch.cuda.synchronize()
+    # the Python mirror of both entry points, outside capture
+    K.release_workspace(s)
+    K.release_workspace(all_streams=True)
+    dec.host_pos(3000, again, s)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
     assert lib.orin_attn_workspace_release_stream(C.c_void_p(s.cuda_stream)) == _lib.OK
