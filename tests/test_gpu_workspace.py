@@ -233,3 +233,57 @@ def test_release_stream():
     torch.cuda.synchronize()
     assert torch.equal(first, again)
     assert lib.orin_attn_workspace_release_stream(C.c_void_p(s.cuda_stream)) == _lib.OK
+
+
+def test_host_threads_on_their_own_streams():
+    """Four host threads, each on its own stream, run growing flash decodes and key-split
+    prefills concurrently (the library call releases the GIL): every output equals the
+    same launch run alone, so the per-stream buffers, the first-use kernel attributes and
+    the buffer growth are safe under concurrent callers."""
+    import threading
+    rng = np.random.default_rng(35)
+    decs = [Decode(rng, max_seq=8192) for _ in range(4)]
+    pre = SplitPrefill(rng)
+    positions = [300, 2000, 5000, 8000]
+    ref_dec = {}
+    for i, d in enumerate(decs):
+        for p in positions:
+            o = d.new_out()
+            d.host_pos(p, o, torch.cuda.current_stream())
+            ref_dec[(i, p)] = o
+    ref_pre = pre.new_out()
+    pre.run(ref_pre, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    K.release_workspace(all_streams=True)  # the threads grow their buffers from nothing
+    errors, results = [], {}
+
+    def work(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for rep in range(3):
+                    for p in positions:
+                        o = decs[i].new_out()
+                        decs[i].host_pos(p, o, s)
+                        results[(i, p, rep)] = o
+                    op = pre.new_out()
+                    pre.run(op, s)
+                    results[(i, "pre", rep)] = op
+            s.synchronize()
+            K.release_workspace(s)
+        except Exception as e:  # surfaced by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for i in range(4):
+        for rep in range(3):
+            for p in positions:
+                assert torch.equal(results[(i, p, rep)], ref_dec[(i, p)]), (i, p, rep)
+            assert torch.equal(results[(i, "pre", rep)], ref_pre), (i, rep)
