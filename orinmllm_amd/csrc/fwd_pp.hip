@@ -455,7 +455,16 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   // row_in_tile * row_bytes + column bytes (`fwd_pp_supports` keeps row_bytes below 2^24,
   // so one 24-bit multiply-add forms it).
   const uint32_t row_bytes = (uint32_t)tok * sizeof(T);
-  auto issue_stage = [&](int u) __attribute__((always_inline)) {
+  // bf16 (plain instance): V is staged through registers, one buffer per ring slot, and
+  // written to LDS converted to fp16 by the step that publishes it, instead of a transfer
+  // to LDS converted there in place; the loads replace the V transfers one for one, so
+  // every wait counts the same.  The ring slot is a compile-time tag at every issue and
+  // conversion, so each load writes its slot's registers directly.  (The fused-Q instance
+  // has no registers to spare and converts in LDS.)
+  constexpr bool kRegV = kConvV && !FQ;
+  u32x4 vbuf[kRegV ? PSTAGES : 1][2];
+  // `sl_tag` = u % PSTAGES as a compile-time constant (used by the register staging).
+  auto issue_stage = [&](int u, auto sl_tag) __attribute__((always_inline)) {
     const int sl = u % PSTAGES;
     // Tile bases are clamped into [0, kv_end - 1] so that the last valid row's offset from
     // its base is never negative: K(n_tiles) of the last stage starts past the sequence and
@@ -474,8 +483,12 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       dma16_s(kt_base, __umul24(rk, row_bytes) + k_col[i] * (uint32_t)sizeof(T),
               k_base + sl * PTILE_BYTES + b * 1024);
       if (u == 0) continue;  // V(-1): no MFMA phase reads it
-      dma16_s(vt_base, __umul24(rv, row_bytes) + v_col[i] * (uint32_t)sizeof(T),
-              k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
+      const uint32_t voff = __umul24(rv, row_bytes) + v_col[i] * (uint32_t)sizeof(T);
+      if constexpr (kRegV)
+        vbuf[decltype(sl_tag)::value % PSTAGES][i] =
+            *reinterpret_cast<const u32x4*>(vt_base + voff);
+      else
+        dma16_s(vt_base, voff, k_base + PKREGION + sl * PTILE_BYTES + b * 1024);
     }
   };
 
@@ -512,10 +525,10 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
 
   // Stages 0 .. PSTAGES-1 up front; wait for stage 0 (younger stages may stay in flight).
-  issue_stage(0);
-#pragma unroll
-  for (int u = 1; u < PSTAGES; ++u)
-    if (n_tiles >= u) issue_stage(u);
+  issue_stage(0, std::integral_constant<int, 0>{});
+  if (n_tiles >= 1) issue_stage(1, std::integral_constant<int, 1>{});
+  if (n_tiles >= 2) issue_stage(2, std::integral_constant<int, 2>{});
+  if (PSTAGES > 3 && n_tiles >= 3) issue_stage(3, std::integral_constant<int, 3 % PSTAGES>{});
   // The fused Q producer works while the first stages are in flight.
   if constexpr (FQ && CAUSAL && (D == 64 || D == 128))
     fuse_q_producer<T, D>(a, qf, qi < q_n, a.start_pos + qi, a.start_pos, hf);
@@ -680,23 +693,30 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   //  fp16: stage u is published by the barrier that ends step 2u-1 and issued at the
   //        start of step 2u-4 (three stages).
   //  bf16: stage u is published one step earlier (end of step 2u-2); at the end of step
-  //        2u-1 every wave converts 1/8 of its V tile to fp16 in place (no phase reads
-  //        stage u in that step), and the barrier ending that step publishes the result;
+  //        2u-1 every wave writes 1/8 of its V tile converted to fp16 (from its registers,
+  //        or in place for the fused-Q instance; no phase reads stage u in that step), and
+  //        the barrier ending that step publishes the result;
   //        it is issued at the start of step 2u-6 (four stages: the slot's previous stage
   //        was last read by group 1's M(u-5) at step 2u-7).
   const int last_step = 2 * n_tiles + 1;
-  auto step_begin = [&](int k) __attribute__((always_inline)) {
+  // `sl_tag`: the ring slot of the stage this step may issue (see the call sites).
+  auto step_begin = [&](int k, auto sl_tag) __attribute__((always_inline)) {
     if (!(k & 1) && k >= 2) {
       const int u = k / 2 + PSTAGES - 1;
-      if (u <= n_tiles) issue_stage(u);
+      if (u <= n_tiles) issue_stage(u, sl_tag);
     }
   };
-  auto convert_v = [&](int u) __attribute__((always_inline)) {
+  auto convert_v = [&](int u, auto sl_tag) __attribute__((always_inline)) {
     // wave w converts bytes [2048 w, 2048 w + 2048) of the stage's V tile
     lds_ptr base = lds0 + PKREGION + (u % PSTAGES) * PTILE_BYTES + wave * 2048 + lane * 16;
     u32x4 x[2];
+    if constexpr (kRegV) {
+      x[0] = vbuf[decltype(sl_tag)::value % PSTAGES][0];
+      x[1] = vbuf[decltype(sl_tag)::value % PSTAGES][1];
+    } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) x[j] = lds_read128(base, j * 1024);
+      for (int j = 0; j < 2; ++j) x[j] = lds_read128(base, j * 1024);
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
@@ -704,14 +724,15 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
           bf16x8_to_f16x8(x[j]);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the writes land before the barrier
   };
-  auto step_end = [&](int k) __attribute__((always_inline)) {
+  // `sl_tag`: the ring slot of the stage this step may convert (see the call sites).
+  auto step_end = [&](int k, auto sl_tag) __attribute__((always_inline)) {
     if constexpr (kConvV) {
       if (!(k & 1)) {
         const int u = k / 2 + 1;
         if (u <= n_tiles) wait_stage(min(n_tiles, k / 2 + PSTAGES - 1) - u);
       } else {
         const int u = (k + 1) / 2;
-        if (u <= n_tiles) convert_v(u);
+        if (u <= n_tiles) convert_v(u, sl_tag);
       }
     } else if (k & 1) {
       const int u = (k + 1) / 2;
@@ -721,34 +742,46 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
     if (k < last_step) step_barrier();
   };
 
+  // Ring-slot tags of the steps (stage u issued at even step 2u - 2(PSTAGES - 1), converted
+  // at odd step 2u - 1, u % PSTAGES its slot): group 1's first step and both groups' QK(0)
+  // step issue nothing and convert stage 1 (slot 1) at most; the softmax(0) step issues
+  // stage PSTAGES (slot 0) in group 1 and converts stage 1 in group 0.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   int k = 0;
   if (grp == 1) {  // group 1 starts one step late
-    step_begin(k);
-    step_end(k);
+    step_begin(k, S0{});
+    step_end(k, S1{});
     ++k;
   }
-  step_begin(k);
+  step_begin(k, S0{});
   qk0();
-  step_end(k);
+  step_end(k, S1{});
   ++k;
-  step_begin(k);
+  step_begin(k, S0{});
   softmax(0);
-  step_end(k);
+  step_end(k, S1{});
   ++k;
   // Tile t's MFMA phase reads ring slot (t+1) % PSTAGES; the loop is unrolled by
   // PSTAGES so every LDS offset is a compile-time constant.  Tiles before the last one always run
   // the QK product of the next tile, also for a wave whose queries all precede it: one
   // MFMA-phase shape inside the loop keeps the accumulators in fixed registers.
+  // In tile t (slot tag (t+1) % PSTAGES) group 0's MFMA step 2t+2 issues stage t +
+  // PSTAGES (slot t % PSTAGES), group 1's softmax step 2t+4 issues stage t + PSTAGES + 1
+  // (slot (t+1) % PSTAGES), and the odd step of each group converts stage t+2.
   auto tile = [&](int t, auto slot_tag) __attribute__((always_inline)) {
-    step_begin(k);
+    constexpr int TG = decltype(slot_tag)::value;
+    using SI = std::integral_constant<int, (TG + PSTAGES - 1) % PSTAGES>;
+    using SC = std::integral_constant<int, (TG + 1) % PSTAGES>;
+    step_begin(k, SI{});
     __builtin_amdgcn_s_setprio(1);
     if (active(t)) mphase(slot_tag, std::true_type{});
     __builtin_amdgcn_s_setprio(0);
-    step_end(k);
+    step_end(k, SC{});
     ++k;
-    step_begin(k);
+    step_begin(k, slot_tag);
     if (active(t + 1)) softmax(t + 1);
-    step_end(k);
+    step_end(k, SC{});
     ++k;
   };
   const int n_loop = n_tiles - 1;
@@ -760,7 +793,7 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
   }
   {  // last tile: PV only
     const int t = n_loop;
-    step_begin(k);
+    step_begin(k, S0{});  // issues nothing: every stage is out
     __builtin_amdgcn_s_setprio(1);
     if (active(t)) {
       switch ((t + 1) % PSTAGES) {
@@ -771,12 +804,12 @@ __global__ void __launch_bounds__(PTHREADS) fwd_pp_kernel(FwdArgs a) {
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    step_end(k);
+    step_end(k, S0{});  // converts nothing: stage n_tiles + 1 does not exist
     ++k;
   }
   if (grp == 0) {  // group 0 ends one step early
-    step_begin(k);
-    step_end(k);
+    step_begin(k, S0{});
+    step_end(k, S0{});
     ++k;
   }
 
