@@ -152,3 +152,22 @@ def test_key_split_close_to_unsplit(kind):
         # Chunks sum their keys in another order than the whole row: the difference is a
         # few roundings of the output type, relative to outputs of order one.
         assert (err <= 2 * ulp * np.abs(part) + 0.5 * ulp).all(), f"{kind} copy {c}: {err.max():.3g}"
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+def test_pp_few_key_tiles(kind):
+    """Segments of 64-320 keys (1 to 5 key tiles per workgroup, on and off the tile edges)
+    x 16 heads: the ring's first stages are also its last, so the stage issue, the waits
+    and (bf16) the register-staged V conversion run their tail cases from the start."""
+    rng = np.random.default_rng(77)
+    H, d = 16, 128
+    seg = [64, 65, 128, 129, 192, 256, 257, 320]
+    cu = np.concatenate([[0], np.cumsum(seg)]).astype(np.int32)
+    q, k, v = vision_inputs(rng, cu, H, d, kind)
+    N = int(cu[-1])
+    out = torch.zeros(N, H * d, device="cuda", dtype=TORCH[kind])
+    K.vision_attention_varlen_cu(dev(q, kind), dev(k, kind), dev(v, kind), out,
+                                 torch.from_numpy(cu).cuda(), max(seg), H, d)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_bidir(q, k, v, cu, nthreads=8)
+    assert_lowp_close(out.float().cpu().numpy(), ref, what=f"pp few tiles {kind}")
